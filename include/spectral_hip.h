@@ -1,0 +1,257 @@
+/*
+ * spectral_hip.h -- C ABI of the MI355X (gfx950) spectral KV-cache library.
+ *
+ * The library replaces the compute path of unsloth-spectral:
+ *   - decode attention over the three-tier cache
+ *       unsloth_spectral/kernels/spectral_attention.py:684-857  (absolute RoPE)
+ *       unsloth_spectral/spectral_attention.py:117-349          (distance RoPE)
+ *   - block compression: randomized SVD + INT8 quantisation
+ *       unsloth_spectral/rsvd.py:28-157
+ *       unsloth_spectral/spectral_cache.py:321-407, 452-516
+ *   - the tier manager (append, compression at the block boundary)
+ *       unsloth_spectral/spectral_cache.py:164-319
+ *
+ * Conventions
+ *   - All tensor arguments are raw device pointers (HBM) plus explicit sizes
+ *     and element strides.  No entry point allocates memory: callers pass a
+ *     workspace where one is needed (size from the matching *_workspace_size).
+ *   - Work is enqueued on the caller's stream (a hipStream_t passed as void*;
+ *     NULL = the null stream).  No entry point synchronises the host.
+ *   - Return value: SC_OK (0) or a negative SC_ERR_* code; sc_last_error()
+ *     returns a thread-local message describing the last failure.
+ *   - FP16 tensors are IEEE binary16 ("half").
+ */
+#ifndef UNSLOTH_SPECTRAL_HIP_H
+#define UNSLOTH_SPECTRAL_HIP_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define SC_ABI_VERSION 1
+
+#define SC_OK 0
+#define SC_ERR_INVALID (-1)      /* bad argument / shape */
+#define SC_ERR_UNSUPPORTED (-2)  /* valid but not implemented for this geometry */
+#define SC_ERR_WORKSPACE (-3)    /* workspace too small */
+#define SC_ERR_HIP (-4)          /* HIP runtime error */
+#define SC_ERR_CAPACITY (-5)     /* tier arrays too small for the request */
+
+/* RoPE alignment of cold keys (tail keys are always rotated at their
+ * absolute position, as in both reference paths). */
+#define SC_ROPE_ABSOLUTE 0 /* kernels/spectral_attention.py:411-446 */
+#define SC_ROPE_DISTANCE 1 /* spectral_attention.py:192-219, d = max(q-p,0) */
+#define SC_ROPE_NONE 2     /* no rotation (bandwidth reference only)    */
+
+/* INT8 scale granularity. */
+#define SC_QUANT_PER_HEAD 0   /* spectral_cache.py:481-516 (reference)     */
+#define SC_QUANT_PER_ROW 1    /* one FP32 scale per token row              */
+#define SC_QUANT_PER_TENSOR 2 /* spectral_cache.py:452-479 (fallback path) */
+
+/* Per-sequence device counters: int32 counters[batch][SC_NCOUNTERS]. */
+#define SC_CNT_NCOLD 0        /* cold blocks in use                      */
+#define SC_CNT_TAIL_HEAD 1    /* ring slot of the oldest tail token      */
+#define SC_CNT_TAIL_LEN 2     /* tokens in the FP16 tail                 */
+#define SC_CNT_NEXT_POS 3     /* reference current_position              */
+#define SC_CNT_TOTAL 4        /* reference total_tokens                  */
+#define SC_CNT_COMPRESSIONS 5 /* reference compression_count             */
+#define SC_NCOUNTERS 8
+
+/*
+ * One layer's cache for `batch` independent sequences (the reference keeps
+ * one SpectralCache per sequence: spectral_cache.py:346).  Layouts
+ * (row-major, innermost last):
+ *   codes_k     int8  [batch][kv_heads][max_blocks][block_size][kp_keys]
+ *   codes_v     int8  [batch][kv_heads][max_blocks][kp_values][block_size]
+ *   scales_k/v  fp32  [batch][kv_heads][max_blocks][block_size]  (PER_ROW)
+ *                     [batch][kv_heads][max_blocks]              (otherwise)
+ *   minmax_k/v  fp32  [batch][kv_heads][max_blocks][2]  reference [min,max]
+ *   vnorm       fp32  [batch][kv_heads][max_blocks]     2^-e, e = exponent
+ *                     of the block's largest V scale (decode prescale)
+ *   basis_k     fp16  [batch][kv_heads][max_blocks][head_dim][kp_keys]
+ *   basis_v     fp16  [batch][kv_heads][max_blocks][kp_values][head_dim]
+ *   block_start int32 [batch][max_blocks]   absolute position of row 0
+ *   tail_k/v    fp16  [batch][kv_heads][tail_capacity][head_dim] (ring,
+ *                     pre-RoPE keys as in spectral_cache.py:172)
+ *   tail_pos    int32 [batch][tail_capacity]
+ *   counters    int32 [batch][SC_NCOUNTERS]
+ * kp_* are the ranks padded to 16, 32 or 64; padded code columns and basis
+ * rows are zero.
+ */
+typedef struct ScTierDesc {
+  int32_t batch, kv_heads, head_dim, block_size;
+  int32_t k_keys, k_values;   /* logical ranks                      */
+  int32_t kp_keys, kp_values; /* storage ranks (16, 32 or 64)       */
+  int32_t max_blocks, tail_capacity, granularity;
+  int8_t* codes_k;
+  int8_t* codes_v;
+  float* scales_k;
+  float* scales_v;
+  float* minmax_k;
+  float* minmax_v;
+  float* vnorm;
+  void* basis_k;
+  void* basis_v;
+  int32_t* block_start;
+  void* tail_k;
+  void* tail_v;
+  int32_t* tail_pos;
+  int32_t* counters;
+} ScTierDesc;
+
+/*
+ * Decode attention for one query token per sequence.
+ * Replaces spectral_attention_decode (kernels/spectral_attention.py:684-857,
+ * rope_mode = SC_ROPE_ABSOLUTE) and spectral_attention_forward
+ * (spectral_attention.py:117-349, rope_mode = SC_ROPE_DISTANCE).
+ *   q          fp16 [batch][q_heads][head_dim] (post-RoPE), element strides
+ *   cos/sin    fp16 [rope_len][head_dim] RoPE tables (row stride rope_stride)
+ *   query_pos  int32 [batch] device array, or NULL to use query_pos_scalar
+ *   mask       optional uint8 keep-mask (0 = drop, reference
+ *              spectral_attention.py:284-285) indexed [b][h][token] in
+ *              cache order (cold blocks, then tail); NULL = no mask
+ *   out        fp16 [batch][q_heads][head_dim]
+ *   logits_out optional fp32 [batch][q_heads][...] = score * scale in cache
+ *              order (testing aid); NULL = not written
+ *   grid_blocks: cold-block slots scanned per sequence (>= every
+ *              counters[b][SC_CNT_NCOLD]); grid_tail: tail tokens scanned
+ *              (>= every counters[b][SC_CNT_TAIL_LEN]).
+ * halves_equal != 0 asserts cos[:, :D/2] == cos[:, D/2:] (HF tables) and
+ * lets the kernel read half rows.
+ */
+typedef struct ScDecodeArgs {
+  const ScTierDesc* tier;
+  int32_t q_heads;
+  int32_t rope_mode;
+  int32_t grid_blocks;
+  int32_t grid_tail;
+  float scale;
+  const void* q;
+  int64_t q_stride_b, q_stride_h;
+  const void* cos;
+  const void* sin;
+  int64_t rope_stride;
+  int32_t rope_len;
+  int32_t halves_equal;
+  const int32_t* query_pos;
+  int32_t query_pos_scalar;
+  const uint8_t* mask;
+  int64_t mask_stride_b, mask_stride_h;
+  void* out;
+  int64_t out_stride_b, out_stride_h;
+  float* logits_out;
+  int64_t logits_stride_b, logits_stride_h;
+} ScDecodeArgs;
+
+int sc_decode_workspace_size(const ScDecodeArgs* args, size_t* bytes);
+int sc_decode_attn(const ScDecodeArgs* args, void* workspace, size_t workspace_bytes,
+                   void* stream);
+
+/*
+ * Batched block compression: randomized SVD (rsvd.py:74-157, k = rank,
+ * oversampling, n_iter) of `count` matrices [rows][cols] (fp16, fp32 or
+ * bf16 per m_dtype; computed in fp32 like rsvd.py:79-81), then
+ * coeffs = U*S (spectral_cache.py:387) quantised to INT8 and basis = Vh in
+ * fp16.  Matrix i = (i / inner, i % inner) is read from
+ *   m + (i/inner)*m_stride_outer + (i%inner)*m_stride_inner, rows m_stride_row
+ * (element strides; rows 16-byte aligned).
+ * omega: fp32 [count][cols][r] Gaussian sketch (r = min(rank+oversample,
+ * rows, cols)); NULL = draw it on the device from `seed` (Philox4x32-10 +
+ * Box-Muller).  Outputs use the same two-level indexing with their strides:
+ *   codes  int8 : coeff_major=0 -> [rows][kp], 1 -> [kp][rows]
+ *   scales fp32 : [rows] (PER_ROW) or [1]
+ *   minmax fp32 : [2] (may be NULL); vnorm fp32 : [1] (may be NULL)
+ *   basis  fp16 : basis_dmajor=1 -> [cols][kp], 0 -> [kp][cols]
+ * Optional fp32 testing outputs (NULL = skipped): coeffs [count][rows][rank],
+ * svals [count][rank], vh [count][rank][cols], omega_out [count][cols][r].
+ * Supported: rows <= 512 (multiple of 64), cols in {64, 128},
+ * rank + oversample <= 40.
+ */
+#define SC_DTYPE_F16 0
+#define SC_DTYPE_F32 1
+#define SC_DTYPE_BF16 2
+
+typedef struct ScCompressArgs {
+  int32_t count, inner;
+  int32_t rows, cols, rank, oversample, n_iter, kp, granularity;
+  int32_t coeff_major, basis_dmajor;
+  int32_t m_dtype; /* SC_DTYPE_*: element type of m */
+  const void* m;
+  int64_t m_stride_outer, m_stride_inner, m_stride_row;
+  const float* omega;
+  uint64_t seed;
+  int8_t* codes;
+  int64_t codes_stride_outer, codes_stride_inner;
+  float* scales;
+  int64_t scales_stride_outer, scales_stride_inner;
+  float* minmax;
+  int64_t minmax_stride_outer, minmax_stride_inner;
+  float* vnorm;
+  int64_t vnorm_stride_outer, vnorm_stride_inner;
+  void* basis;
+  int64_t basis_stride_outer, basis_stride_inner;
+  float* coeffs_out;
+  float* svals_out;
+  float* vh_out;
+  float* omega_out;
+} ScCompressArgs;
+
+int sc_rsvd_compress(const ScCompressArgs* args, void* stream);
+
+/*
+ * INT8 symmetric quantisation of fp32 x [groups][rows][cols]
+ * (spectral_cache.py:452-516): PER_HEAD -> one scale per group,
+ * PER_ROW -> one per row, PER_TENSOR -> one in total.
+ * scale = max(absmax, 1e-8)/127 (IEEE), code = round_half_even(x/scale).
+ * codes int8 like x; scales fp32 [groups] / [groups][rows] / [1];
+ * minmax fp32 [groups][2] (may be NULL).
+ */
+int sc_quantize_int8(const float* x, int64_t groups, int64_t rows, int64_t cols,
+                     int32_t granularity, int8_t* codes, float* scales, float* minmax,
+                     void* stream);
+
+/*
+ * Append t_new tokens to every sequence's FP16 tail (spectral_cache.py:164-232):
+ *   k_new, v_new fp16 [batch][kv_heads][t_new][head_dim] with element
+ *   strides (stride_b, stride_h, stride_t; innermost contiguous);
+ *   positions int32 [batch][t_new] (NULL = continue from NEXT_POS).
+ * A first position below NEXT_POS resets the sequence's counters first
+ * (new-generation detection, spectral_cache.py:176-189).
+ * Fails with SC_ERR_CAPACITY (before launching) if t_new exceeds the ring.
+ */
+int sc_tier_append(const ScTierDesc* tier, const void* k_new, const void* v_new,
+                   int64_t stride_b, int64_t stride_h, int64_t stride_t,
+                   const int32_t* positions, int32_t t_new, void* stream);
+
+/*
+ * Compress every full block of every sequence's tail into the next cold
+ * slots (spectral_cache.py:243-319), K with rank k_keys and V with k_values,
+ * then advance NCOLD / TAIL_HEAD / TAIL_LEN / COMPRESSIONS on the device.
+ * max_new_blocks bounds the blocks compressed per sequence in this call
+ * (grid size); sequences with fewer full blocks compress what they have.
+ * Compression happens only where counters say a block is full, so the
+ * call may be enqueued speculatively.  seed drives the Gaussian sketch
+ * (block j of sequence b, head h, K/V get distinct Philox streams).
+ */
+int sc_tier_compress(const ScTierDesc* tier, int32_t max_new_blocks, int32_t n_iter,
+                     int32_t oversample, uint64_t seed, void* stream);
+
+/*
+ * Dequantise cold blocks [first, first+count) of every sequence into fp16
+ * K/V [batch][kv_heads][count*block_size][head_dim] (get_kv,
+ * spectral_cache.py:557-612; reference coefficients are fp16(code*scale)).
+ */
+int sc_tier_dequant(const ScTierDesc* tier, int32_t first, int32_t count, void* k_out,
+                    void* v_out, void* stream);
+
+const char* sc_last_error(void);
+int sc_abi_version(void);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* UNSLOTH_SPECTRAL_HIP_H */

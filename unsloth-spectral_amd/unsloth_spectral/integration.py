@@ -1,0 +1,274 @@
+"""Model integration: per-layer spectral cache behind the attention module.
+
+API of unsloth_spectral/integration.py: ``create_spectral_forward``
+(:43-425), ``apply_rotary_pos_emb`` (:428-465), ``repeat_kv`` (:468-478),
+``create_spectral_forward_inference`` (:481-725), ``patch_unsloth_attention``
+(:728-889), ``get_cache_stats`` (:892-938).
+
+Order of operations per layer and step (integration.py:596-659): project
+Q/K/V, rotate Q (and K for the dense prefill), append the *pre-RoPE* K and V
+to the layer's SpectralCache (compression fires inside append), then attend.
+One-token decode steps run the fused HIP kernel over all tiers (cold blocks
+and FP16 tail, so the reference's ``total_tokens > block_size`` branch and
+its dense fallback are the same kernel with zero or more cold blocks).
+Multi-token (prefill) steps run dense causal attention over the cache's
+reconstruction (``get_kv``), as the reference does (:292-346).
+
+The patched forward accepts the attention signature of transformers 5.x
+(``position_embeddings=(cos, sin)`` for the current tokens, cache in the
+module) and keeps each layer's SpectralCache on the module; full RoPE
+tables for the cached positions come from the model's rotary module.
+"""
+import logging
+import math
+from typing import Optional
+
+import torch
+import torch.nn.functional as F
+
+from . import _lib
+from ._decode import run_decode
+from .spectral_attention import apply_rope, repeat_kv as _repeat_kv
+from .spectral_cache import SpectralCache
+
+logger = logging.getLogger("unsloth_spectral.integration")
+
+TRITON_KERNELS_AVAILABLE = False
+
+
+def rotate_half(x):
+    h = x.shape[-1] // 2
+    return torch.cat((-x[..., h:], x[..., :h]), dim=-1)
+
+
+def apply_rotary_pos_emb(q, k, cos, sin, position_ids=None):
+    """HF rotate_half RoPE (integration.py:428-465); cos/sin [T, D] or [B, T, D]."""
+    if cos.dim() == 2:
+        cos, sin = cos[None, None], sin[None, None]
+    elif cos.dim() == 3:
+        cos, sin = cos[:, None], sin[:, None]
+    return q * cos + rotate_half(q) * sin, k * cos + rotate_half(k) * sin
+
+
+def repeat_kv(hidden_states: torch.Tensor, n_rep: int) -> torch.Tensor:
+    return _repeat_kv(hidden_states, n_rep)
+
+
+class _RopeTable:
+    """Full cos/sin tables [L, D] (fp16) for absolute positions, built with
+    the model's own rotary module so the values equal what the model uses."""
+
+    def __init__(self, rotary, head_dim, theta=None):
+        self.rotary = rotary
+        self.head_dim = head_dim
+        self.theta = theta
+        self.cos = None
+        self.sin = None
+
+    def get(self, length, device):
+        if self.cos is None or self.cos.shape[0] < length or self.cos.device != device:
+            L = 1 << max(12, (int(length) - 1).bit_length())
+            pos = torch.arange(L, device=device)
+            if self.rotary is not None:
+                dummy = torch.zeros(1, 1, self.head_dim, dtype=torch.float16, device=device)
+                c, s = self.rotary(dummy, pos[None])
+                c, s = c[0], s[0]
+            else:
+                inv = 1.0 / (self.theta ** (torch.arange(0, self.head_dim, 2, device=device).float()
+                                            / self.head_dim))
+                emb = torch.cat([torch.outer(pos.float(), inv)] * 2, dim=-1)
+                c, s = emb.cos(), emb.sin()
+            self.cos = c.to(torch.float16).contiguous()
+            self.sin = s.to(torch.float16).contiguous()
+        return self.cos, self.sin
+
+
+def _model_rope(module, head_dim):
+    tab = getattr(module, "_spectral_rope", None)
+    if tab is None:
+        theta = getattr(getattr(module, "config", None), "rope_theta", None) or 10000.0
+        tab = _RopeTable(getattr(module, "rotary_emb", None), head_dim, theta)
+        module._spectral_rope = tab
+    return tab
+
+
+def _dense_prefill(q_rot, cache, cos_tab, sin_tab, n_rep, attention_mask, scale):
+    """Dense causal attention over get_kv() with keys rotated at their
+    absolute positions (integration.py:297-346)."""
+    K, V = cache.get_kv()
+    pos = cache.get_all_positions()
+    K = apply_rope(K, cos_tab[pos][None, None], sin_tab[pos][None, None])
+    K = _repeat_kv(K, n_rep)
+    V = _repeat_kv(V, n_rep)
+    T, L = q_rot.shape[2], K.shape[2]
+    if attention_mask is not None and attention_mask.dim() == 4 and attention_mask.shape[-1] == L \
+            and attention_mask.dtype != torch.bool:
+        mask = attention_mask[..., -T:, :].to(q_rot.dtype)
+        return F.scaled_dot_product_attention(q_rot, K, V, attn_mask=mask, scale=scale)
+    causal = torch.ones(T, L, dtype=torch.bool, device=q_rot.device).tril(L - T)
+    return F.scaled_dot_product_attention(q_rot, K, V, attn_mask=causal, scale=scale)
+
+
+def _cache_for(module, num_kv, head_dim, dtype, device, opts):
+    cache = getattr(module, "_spectral_cache", None)
+    if not isinstance(cache, SpectralCache) or cache.head_dim != head_dim or cache.device != device:
+        cache = SpectralCache(num_heads=num_kv, head_dim=head_dim, block_size=opts["block_size"],
+                              k_rank_keys=opts["k_rank_keys"], k_rank_values=opts["k_rank_values"],
+                              hot_buffer_size=opts["hot_buffer_size"], device=device, dtype=torch.float16,
+                              debug_logging=opts["debug_logging"],
+                              use_attention_weighted_svd=opts["use_attention_weighted_svd"],
+                              landmark_count=opts["landmark_count"],
+                              quant_granularity=opts.get("quant_granularity", "per_head"))
+        module._spectral_cache = cache
+    return cache
+
+
+def _attend(self, hidden_states, cos_cur, sin_cur, position_ids, attention_mask, opts, rope_mode):
+    cfg = self.config
+    Hq, Hkv = cfg.num_attention_heads, cfg.num_key_value_heads
+    D = getattr(self, "head_dim", None) or cfg.hidden_size // Hq
+    B, T, _ = hidden_states.shape
+    q = self.q_proj(hidden_states).view(B, T, Hq, D).transpose(1, 2)
+    k = self.k_proj(hidden_states).view(B, T, Hkv, D).transpose(1, 2)
+    v = self.v_proj(hidden_states).view(B, T, Hkv, D).transpose(1, 2)
+    cache = _cache_for(self, Hkv, D, hidden_states.dtype, hidden_states.device, opts)
+    if position_ids is None:
+        start = cache.current_position
+        position_ids = torch.arange(start, start + T, device=hidden_states.device)[None].expand(B, T)
+    tab = _model_rope(self, D)
+    if cos_cur is None:
+        cos_all, sin_all = tab.get(cache.current_position + T + 1, hidden_states.device)
+        cos_cur, sin_cur = cos_all[position_ids], sin_all[position_ids]
+    q_rot = (q * cos_cur[:, None] + rotate_half(q) * sin_cur[:, None]).to(torch.float16)
+    cache.append(k, v, position_ids)                       # pre-RoPE K (integration.py:618-624)
+    cos_tab, sin_tab = tab.get(cache.current_position + 1, hidden_states.device)
+    scale = getattr(self, "scaling", None) or 1.0 / math.sqrt(D)
+    if T == 1 and opts["use_spectral_attention"]:
+        qpos = position_ids[:, -1]
+        out = run_decode(q_rot, cache, cos_tab, sin_tab, qpos, None, scale, rope_mode, halves_equal=True)
+    else:
+        out = _dense_prefill(q_rot, cache, cos_tab, sin_tab, Hq // Hkv, attention_mask, scale)
+    out = out.to(hidden_states.dtype).transpose(1, 2).reshape(B, T, Hq * D)
+    return self.o_proj(out), cache
+
+
+def _options(block_size, k_rank_keys, k_rank_values, hot_buffer_size, use_spectral_attention, debug_logging,
+             use_attention_weighted_svd, landmark_count, quant_granularity="per_head"):
+    return dict(block_size=block_size, k_rank_keys=k_rank_keys, k_rank_values=k_rank_values,
+                hot_buffer_size=hot_buffer_size, use_spectral_attention=use_spectral_attention,
+                debug_logging=debug_logging, use_attention_weighted_svd=use_attention_weighted_svd,
+                landmark_count=landmark_count, quant_granularity=quant_granularity)
+
+
+def create_spectral_forward(original_forward, block_size=512, k_rank_keys=16, k_rank_values=32,
+                            hot_buffer_size=64, use_spectral_attention=True, debug_logging=False,
+                            use_attention_weighted_svd=False, landmark_count=0, rope_mode=None,
+                            quant_granularity="per_head"):
+    """Forward for an HF-style attention module (integration.py:43-425).
+    Accepts both the transformers 5.x signature (position_embeddings) and
+    the older one (position_ids, past_key_value)."""
+    opts = _options(block_size, k_rank_keys, k_rank_values, hot_buffer_size, use_spectral_attention,
+                    debug_logging, use_attention_weighted_svd, landmark_count, quant_granularity)
+    mode = _lib.SC_ROPE_DISTANCE if rope_mode is None else rope_mode   # reference HF path: distance (:283)
+
+    def spectral_forward(self, hidden_states, position_embeddings=None, attention_mask=None,
+                         past_key_values=None, **kwargs):
+        position_ids = kwargs.get("position_ids")
+        if position_ids is None and kwargs.get("cache_position") is not None:
+            position_ids = kwargs["cache_position"][None].expand(hidden_states.shape[0], -1)
+        cos_cur = sin_cur = None
+        if position_embeddings is not None:
+            cos_cur, sin_cur = position_embeddings
+        out, cache = _attend(self, hidden_states, cos_cur, sin_cur, position_ids, attention_mask, opts, mode)
+        return out, None
+
+    return spectral_forward
+
+
+def create_spectral_forward_inference(block_size=512, k_rank_keys=16, k_rank_values=32, hot_buffer_size=64,
+                                      use_spectral_attention=True, debug_logging=False, use_triton_kernel=True,
+                                      use_attention_weighted_svd=False, landmark_count=0):
+    """Unsloth-signature decode function (integration.py:481-725):
+    (self, hidden_states, past_key_value, position_ids, do_prefill, attention_mask)
+    -> (attn_output, cache).  use_triton_kernel selects the absolute-RoPE
+    path (the reference's Triton-module branch), otherwise distance RoPE."""
+    opts = _options(block_size, k_rank_keys, k_rank_values, hot_buffer_size, use_spectral_attention,
+                    debug_logging, use_attention_weighted_svd, landmark_count)
+    mode = _lib.SC_ROPE_ABSOLUTE if use_triton_kernel else _lib.SC_ROPE_DISTANCE
+
+    def spectral_forward_inference(self, hidden_states, past_key_value, position_ids, do_prefill=False,
+                                   attention_mask=None):
+        if isinstance(past_key_value, SpectralCache):
+            self._spectral_cache = past_key_value
+        out, cache = _attend(self, hidden_states, None, None, position_ids, attention_mask, opts, mode)
+        return out, cache
+
+    return spectral_forward_inference
+
+
+def patch_unsloth_attention(model, block_size: int = 512, k_rank_keys: int = 16, k_rank_values: int = 32,
+                            hot_buffer_size: int = 64, use_spectral_attention: bool = True, verbose: bool = True,
+                            debug_logging: bool = False, use_triton_kernel: bool = True,
+                            use_attention_weighted_svd: bool = False, landmark_count: int = 0,
+                            quant_granularity: str = "per_head"):
+    """Patches every ``model.model.layers[i].self_attn`` (integration.py:728-889).
+    The decode path uses the absolute-RoPE kernel when ``use_triton_kernel``
+    (the reference's default branch), distance RoPE otherwise."""
+    _lib.load()
+    rotary = getattr(getattr(model, "model", model), "rotary_emb", None)
+    mode = _lib.SC_ROPE_ABSOLUTE if use_triton_kernel else _lib.SC_ROPE_DISTANCE
+    n = 0
+    for layer in model.model.layers:
+        attn = getattr(layer, "self_attn", None)
+        if attn is None:
+            continue
+        fwd = create_spectral_forward(attn.forward, block_size, k_rank_keys, k_rank_values, hot_buffer_size,
+                                      use_spectral_attention, debug_logging, use_attention_weighted_svd,
+                                      landmark_count, rope_mode=mode, quant_granularity=quant_granularity)
+        attn.forward = fwd.__get__(attn, type(attn))
+        attn._spectral_rope = _RopeTable(rotary, getattr(attn, "head_dim", None) or
+                                         model.config.hidden_size // model.config.num_attention_heads,
+                                         getattr(model.config, "rope_theta", 10000.0))
+        attn._spectral_cache = None
+        n += 1
+    try:
+        import unsloth.models.llama as llama_module  # noqa: F401
+        llama_module.LlamaAttention_fast_forward_inference = create_spectral_forward_inference(
+            block_size, k_rank_keys, k_rank_values, hot_buffer_size, use_spectral_attention, debug_logging,
+            use_triton_kernel, use_attention_weighted_svd, landmark_count)
+        if hasattr(llama_module, "_LlamaModel_fast_forward_inference"):
+            llama_module.LlamaModel_fast_forward_inference = llama_module._LlamaModel_fast_forward_inference(
+                attention_fast_forward_inference=llama_module.LlamaAttention_fast_forward_inference)
+    except Exception as e:  # unsloth absent: the HF-style forward covers decode
+        if verbose:
+            print(f"(unsloth fast path not patched: {e.__class__.__name__}; HF-style forward in use)")
+    if verbose:
+        print(f"Patched {n} attention layers with SpectralCache (HIP)")
+        print(f"   Config: block_size={block_size}, k_K={k_rank_keys}, k_V={k_rank_values}")
+    return model
+
+
+def reset_spectral_caches(model):
+    """Drops every layer's cache (start of a new generation)."""
+    for layer in model.model.layers:
+        if hasattr(layer, "self_attn"):
+            layer.self_attn._spectral_cache = None
+
+
+def get_cache_stats(model):
+    """integration.py:892-938"""
+    total_tokens = total_blocks = orig = comp = 0
+    per_layer = []
+    for i, layer in enumerate(model.model.layers):
+        cache = getattr(getattr(layer, "self_attn", None), "_spectral_cache", None)
+        if isinstance(cache, SpectralCache):
+            s = cache.get_memory_stats()
+            total_tokens += s["total_tokens"]
+            total_blocks += s["num_blocks"]
+            orig += s["original_bytes"]
+            comp += s["compressed_bytes"]
+            per_layer.append({"layer_idx": i, "tokens": s["total_tokens"], "blocks": s["num_blocks"],
+                              "compression": s["compression_ratio"]})
+    return {"total_tokens": total_tokens, "total_blocks": total_blocks, "total_original_bytes": orig,
+            "total_compressed_bytes": comp, "compression_ratio": orig / comp if comp > 0 else 1.0,
+            "layers_with_cache": len(per_layer), "per_layer_stats": per_layer}
