@@ -71,15 +71,18 @@ class Hip:
 
 
 def lowrank_kv(torch, seed, n, ctx, d, device, unit_scale=False):
-    g = torch.Generator(device=device)
+    """n matrices U diag(sigma) V^T + 0.01 N(0,1), sigma_i = exp(-i/8), U and V
+    the Q factors of Gaussian draws.  Generated on the host (seeded CPU
+    generator, LAPACK QR) so the data do not depend on the GPU's libraries."""
+    g = torch.Generator()
     g.manual_seed(seed)
-    sig = torch.exp(-torch.arange(d, device=device, dtype=torch.float32) / 8.0)
+    sig = torch.exp(-torch.arange(d, dtype=torch.float32) / 8.0)
     lift = math.sqrt(ctx * d / float((sig ** 2).sum())) if unit_scale else 1.0
     out = torch.empty(n, ctx, d, dtype=torch.float16, device=device)
     for i in range(n):
-        U, _ = torch.linalg.qr(torch.randn(ctx, d, generator=g, device=device))
-        V, _ = torch.linalg.qr(torch.randn(d, d, generator=g, device=device))
-        out[i] = ((U * (sig * lift)) @ V.T + 0.01 * torch.randn(ctx, d, generator=g, device=device)).half()
+        U, _ = torch.linalg.qr(torch.randn(ctx, d, generator=g))
+        V, _ = torch.linalg.qr(torch.randn(d, d, generator=g))
+        out[i] = ((U * (sig * lift)) @ V.T + 0.01 * torch.randn(ctx, d, generator=g)).half().to(device)
     return out
 
 
@@ -142,7 +145,7 @@ def cpu_decode_baseline(cache, Q, cos, sin):
     sk = cache.scales_k[0, :, :nb].cpu().numpy()
     sv = cache.scales_v[0, :, :nb].cpu().numpy()
     bk = cache.basis_k[0, :, :nb, :, :K_RANK].transpose(-1, -2).cpu().numpy()
-    bv = cache.basis_v[0, :, :nb, :K_RANK, :].cpu().numpy()
+    bv = cache.basis_v[0, :, :nb, :, :K_RANK].transpose(-1, -2).cpu().numpy()
     blocks = [ColdBlock(ck[:, j], sk[:, j], bk[:, j], cv[:, j], sv[:, j], bv[:, j], j * TB) for j in range(nb)]
     st = TierState(blocks, cache.hot_K[0].cpu().numpy(), cache.hot_V[0].cpu().numpy(),
                    cache.hot_position_ids[0].cpu().numpy())

@@ -72,7 +72,7 @@ extern "C" {
  *   vnorm       fp32  [batch][kv_heads][max_blocks]     2^-e, e = exponent
  *                     of the block's largest V scale (decode prescale)
  *   basis_k     fp16  [batch][kv_heads][max_blocks][head_dim][kp_keys]
- *   basis_v     fp16  [batch][kv_heads][max_blocks][kp_values][head_dim]
+ *   basis_v     fp16  [batch][kv_heads][max_blocks][head_dim][kp_values]
  *   block_start int32 [batch][max_blocks]   absolute position of row 0
  *   tail_k/v    fp16  [batch][kv_heads][tail_capacity][head_dim] (ring,
  *                     pre-RoPE keys as in spectral_cache.py:172)

@@ -25,7 +25,7 @@ def export_states(cache):
     sk = cache.scales_k[:, :, :nb].cpu().numpy()
     sv = cache.scales_v[:, :, :nb].cpu().numpy()
     bk = cache.basis_k[:, :, :nb, :, :kK].transpose(-1, -2).cpu().numpy()
-    bv = cache.basis_v[:, :, :nb, :kV, :].cpu().numpy()
+    bv = cache.basis_v[:, :, :nb, :, :kV].transpose(-1, -2).cpu().numpy()
     starts = cache.block_start[:, :nb].cpu().numpy()
     hk, hv, hp = cache.hot_K, cache.hot_V, cache.hot_position_ids
     out = []

@@ -33,17 +33,28 @@ static inline int sc_launch_status(const char* what) {
 // ------------------------------------------------------------- wavefront
 __device__ __forceinline__ int lane_id() { return threadIdx.x & 63; }
 
-// Butterfly over lanes that differ in bits 4 and 5 (the four 16-lane rows of
-// a wavefront): combines the values that MFMA 16x16 outputs spread over rows.
+// Reductions over the four 16-lane rows of a wavefront (lanes n, n+16,
+// n+32, n+48): combine the values that MFMA 16x16 outputs spread over rows.
+// gfx950's v_permlane32_swap exchanges lanes 32-63 of one register with
+// lanes 0-31 of another; applied to two copies of v it leaves (lo, lo) and
+// (hi, hi), so op(first, second) holds op(lo, hi) in every lane.  The
+// 16-lane variant does the same between odd and even rows.  Both are VALU
+// operations (no LDS round trip).
 __device__ __forceinline__ float max_over_rows(float v) {
-  v = fmaxf(v, __shfl_xor(v, 16));
-  v = fmaxf(v, __shfl_xor(v, 32));
-  return v;
+  const uint32_t u = __float_as_uint(v);
+  auto a = __builtin_amdgcn_permlane32_swap(u, u, false, false);
+  v = fmaxf(__uint_as_float(a[0]), __uint_as_float(a[1]));
+  const uint32_t w = __float_as_uint(v);
+  auto b = __builtin_amdgcn_permlane16_swap(w, w, false, false);
+  return fmaxf(__uint_as_float(b[0]), __uint_as_float(b[1]));
 }
 __device__ __forceinline__ float sum_over_rows(float v) {
-  v += __shfl_xor(v, 16);
-  v += __shfl_xor(v, 32);
-  return v;
+  const uint32_t u = __float_as_uint(v);
+  auto a = __builtin_amdgcn_permlane32_swap(u, u, false, false);
+  v = __uint_as_float(a[0]) + __uint_as_float(a[1]);
+  const uint32_t w = __float_as_uint(v);
+  auto b = __builtin_amdgcn_permlane16_swap(w, w, false, false);
+  return __uint_as_float(b[0]) + __uint_as_float(b[1]);
 }
 __device__ __forceinline__ float wave_max(float v) {
 #pragma unroll

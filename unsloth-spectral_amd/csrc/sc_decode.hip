@@ -5,26 +5,36 @@
 //   spectral_attention_forward  spectral_attention.py:117-349          (distance RoPE)
 // with one split-K kernel plus a log-sum-exp combine.
 //
-// Work unit = (sequence b, KV head h, chunk).  A chunk is one cold block
-// (block_size tokens) or 64 tail tokens.  A unit runs on one 256-thread
-// workgroup; wave w owns a quarter of the chunk and walks it in tiles of 16
-// tokens.  Per cold tile and KV head:
-//   1. codes (INT8, token-major) -> fp16 in registers (exact), and
-//      X^T = B_K^T . code^T on MFMA 16x16x32 (the basis of the block is
-//      held in VGPRs for the whole block; its rows are permuted so that a
-//      lane ends up with a token's d and d+D/2 entries -- a RoPE pair).
-//   2. RoPE of the reconstructed key, in packed fp16: R_phi(x), with
-//      phi = p (absolute) or max(q-p,0) (distance), cos/sin rows of the
-//      caller's table.  Row scale s_t is applied after the dot (linear).
-//   3. scores of the whole GQA group: S = Y . Q^T on MFMA (Q in VGPRs).
-//   4. online softmax in the log2 domain, row-group butterflies.
-//   5. P . C_V accumulated on MFMA 16x16x16 with the per-token V scale
-//      folded into P (prescaled by the block's power-of-two vnorm), codes
-//      of V stored coefficient-major so each lane reads 4 contiguous bytes.
-// At the end of the block the four waves merge in LDS and the merged
-// (P.C_V) of every query head is projected once through B_V.
-// Tail chunks skip step 1 (fp16 keys) and use P . V directly.
+// Work unit = (sequence b, KV head h, chunk); one 256-thread workgroup.  A
+// cold chunk is up to 512 tokens of one cold block; wave w owns 16*TPW
+// consecutive tokens of it.  A tail chunk is 128 FP16 tail tokens.
+//
+// Cold path, per wave (two phases over the wave's tiles of 16 tokens):
+//   0. every HBM load of the wave is issued up front (INT8 codes of K and V,
+//      per-row scales, the K basis as MFMA operands, Q), so a workgroup
+//      keeps its whole share of the block in flight at once;
+//   A. per tile: X^T = B_K^T . code^T on MFMA (codes -> fp16 exactly in
+//      registers; basis rows permuted so that a lane holds the RoPE pairs
+//      (d, d + D/2) of one token), RoPE of the reconstructed key in packed
+//      fp16 with the caller's cos/sin rows (phi = p, or max(q - p, 0) in
+//      distance mode), scores of the GQA group S = Y . Q^T on MFMA, times
+//      the row scale, rounded at the reference's fp16 cast points;
+//   B. one maximum over all the wave's scores (no running rescale);
+//   C. per tile: P = exp2(logit - max), Pacc^T += C_V^T . (P * s_V) on MFMA.
+// Token order inside a 64-token group is permuted (lane group g of a score
+// tile holds tokens 16g + 4i + j of tile i) so that the V codes of four
+// tiles are one 16-byte load per lane and per-row scales are one coalesced
+// load per 64 tokens, broadcast with ds_swizzle.  The four waves merge in
+// LDS and the merged P.C_V of every query head is projected once through
+// B_V (d-major).
+//
+// GEN = false is the branch-free path (RoPE absolute or distance over an
+// HF table whose halves are equal, no mask, no logits output); GEN = true
+// adds the keep-mask, the logits output, unequal table halves and
+// rope_mode = none.
 #include <math.h>
+
+#include <type_traits>
 
 #include "sc_common.h"
 
@@ -33,13 +43,18 @@ namespace {
 constexpr int kWaves = 4;
 constexpr int kThreads = 64 * kWaves;
 constexpr int kTile = 16;
-constexpr int kTailUnit = kWaves * kTile;  // tail tokens per unit
-constexpr int kMaxRep = 16;                // query heads per KV head (MFMA N)
+constexpr int kMaxRep = 16;
+constexpr int kTailTiles = 2;                           // tail tiles per wave
+constexpr int kTailUnit = kWaves * kTailTiles * kTile;  // tail tokens per unit
+constexpr int kVRow = 132;                              // LDS row (halves) of a staged V tile
+constexpr int kCombineWaves = 16;
+constexpr float kLog2e = 1.4426950408889634f;
 
 struct DecodeParams {
   int B, Hq, Hkv, nrep, TB, NB, TCAP, per_row, rope_mode, rope_len, halves_equal;
-  int grid_blocks, tail_units, units_per_bh, total_units;
-  float scale, scale_log2;
+  int grid_blocks, tpw, n_hq, cold_units, tail_units, units_per_bh;
+  long n_cold_units, n_tail_units;  // summed over (b, h)
+  float scale;
   const h16* q;
   long q_sb, q_sh;
   const int8_t* codes_k;
@@ -72,74 +87,86 @@ struct DecodeParams {
 //   cold, absolute : (c1 x1 - s2 x2, s1 x1 + c2 x2)  from Q . R_{-p} (_apply_inverse_rope)
 //   tail, absolute : (c1 x1 - s1 x2, s2 x1 + c2 x2)  _apply_rope on the key
 //   distance       : (c1 x1 - s1 x2, s1 x1 + c1 x2)  apply_rope (first half only)
+// With equal halves (c1 = c2, s1 = s2) all three are (c x1 - s x2, s x1 + c x2).
 enum RotKind { kRotColdAbs = 0, kRotTailAbs = 1, kRotDist = 2 };
 
 template <int D>
 struct Geo {
   static constexpr int HALF = D / 2;
-  static constexpr int QG = HALF / 4;     // pairs per lane
-  static constexpr int NP = QG / 2;       // half2 pairs per lane
-  static constexpr int MT = D / 16;       // 16-row tiles over d
+  static constexpr int QG = HALF / 4;  // RoPE pairs per lane
+  static constexpr int NV = QG / 8;    // half8 vectors per lane and half
+  static constexpr int MT = D / 16;    // 16-row tiles over d
   static constexpr int MTH = MT / 2;
-  static constexpr int DS = D / 32;       // K-steps of the score MFMA
-  static constexpr int PREC = D + 2;      // partial record: m, l, o[D]
+  static constexpr int DS = D / 32;    // K-steps of the score MFMA (= 2 NV)
+  static constexpr int PREC = D + 4;   // partial record: m, l, -, -, o[D] (o 16-byte aligned)
 };
 
-// Loads QG consecutive fp16 (QG = 8 or 16) as half2 pairs.
-template <int QG>
-__device__ __forceinline__ void load_pairs(const h16* src, half2_t (&dst)[QG / 2]) {
+template <int NV>
+struct Half8s {
+  half8_t v[NV];
+};
+
+template <int NV>
+__device__ __forceinline__ Half8s<NV> load_h8s(const h16* src) {
+  Half8s<NV> r;
 #pragma unroll
-  for (int v = 0; v < QG / 8; ++v) {
-    half8_t t = *reinterpret_cast<const half8_t*>(src + 8 * v);
+  for (int i = 0; i < NV; ++i) r.v[i] = *reinterpret_cast<const half8_t*>(src + 8 * i);
+  return r;
+}
+
+// Packs the reconstruct MFMA outputs of one lane into the x1 / x2 halves:
+// x1 element 4*mt + j = x[mt][j] (mt < MTH), x2 from x[MTH + mt].
+template <int D>
+__device__ __forceinline__ void pack_x(const float4_t (&x)[Geo<D>::MT], Half8s<Geo<D>::NV>& x1,
+                                       Half8s<Geo<D>::NV>& x2) {
+  using G = Geo<D>;
 #pragma unroll
-    for (int e = 0; e < 4; ++e) dst[4 * v + e] = (half2_t){t[2 * e], t[2 * e + 1]};
+  for (int v = 0; v < G::NV; ++v) {
+    const float4_t a = x[2 * v], b = x[2 * v + 1], c = x[G::MTH + 2 * v], d = x[G::MTH + 2 * v + 1];
+    x1.v[v] = (half8_t){(h16)a[0], (h16)a[1], (h16)a[2], (h16)a[3], (h16)b[0], (h16)b[1], (h16)b[2], (h16)b[3]};
+    x2.v[v] = (half8_t){(h16)c[0], (h16)c[1], (h16)c[2], (h16)c[3], (h16)d[0], (h16)d[1], (h16)d[2], (h16)d[3]};
   }
 }
 
-// Rotates the lane's QG pairs in packed fp16 and packs the result as the
-// A operand (per K-step of 8) of the score MFMA.
+// Rotated key as the A operand of the score MFMA (K-step s < DS/2 -> first
+// half, else second half).  c1/s1 are the lane's first-half table entries;
+// c2/s2 its second-half entries (== c1/s1 when the halves are equal).
 template <int D>
-__device__ __forceinline__ void rotate_pairs(const half2_t (&x1)[Geo<D>::NP], const half2_t (&x2)[Geo<D>::NP],
-                                             const h16* crow, const h16* srow, int g, int kind,
-                                             bool halves_equal, half8_t (&ya)[Geo<D>::DS]) {
+__device__ __forceinline__ void rotate(const Half8s<Geo<D>::NV>& x1, const Half8s<Geo<D>::NV>& x2,
+                                       const Half8s<Geo<D>::NV>& c1, const Half8s<Geo<D>::NV>& s1,
+                                       const Half8s<Geo<D>::NV>& c2, const Half8s<Geo<D>::NV>& s2, int kind,
+                                       half8_t (&ya)[Geo<D>::DS]) {
   using G = Geo<D>;
-  half2_t c1[G::NP], s1[G::NP], c2[G::NP], s2[G::NP];
-  load_pairs<G::QG>(crow + g * G::QG, c1);
-  load_pairs<G::QG>(srow + g * G::QG, s1);
-  if (!halves_equal && kind != kRotDist) {
-    load_pairs<G::QG>(crow + G::HALF + g * G::QG, c2);
-    load_pairs<G::QG>(srow + G::HALF + g * G::QG, s2);
-  } else {
 #pragma unroll
-    for (int e = 0; e < G::NP; ++e) {
-      c2[e] = c1[e];
-      s2[e] = s1[e];
-    }
-  }
-  half2_t y1[G::NP], y2[G::NP];
-#pragma unroll
-  for (int e = 0; e < G::NP; ++e) {
-    const half2_t sa = (kind == kRotColdAbs) ? s2[e] : s1[e];
-    const half2_t sb = (kind == kRotTailAbs) ? s2[e] : s1[e];
-    const half2_t cb = (kind == kRotDist) ? c1[e] : c2[e];
-    y1[e] = c1[e] * x1[e] - sa * x2[e];
-    y2[e] = sb * x1[e] + cb * x2[e];
-  }
-#pragma unroll
-  for (int s = 0; s < G::DS; ++s) {
-    const half2_t* src = (s < G::DS / 2) ? &y1[4 * s] : &y2[4 * (s - G::DS / 2)];
-    ya[s] = (half8_t){src[0].x, src[0].y, src[1].x, src[1].y, src[2].x, src[2].y, src[3].x, src[3].y};
+  for (int v = 0; v < G::NV; ++v) {
+    const half8_t sa = (kind == kRotColdAbs) ? s2.v[v] : s1.v[v];
+    const half8_t sb = (kind == kRotTailAbs) ? s2.v[v] : s1.v[v];
+    const half8_t cb = (kind == kRotDist) ? c1.v[v] : c2.v[v];
+    ya[v] = c1.v[v] * x1.v[v] - sa * x2.v[v];
+    ya[G::NV + v] = sb * x1.v[v] + cb * x2.v[v];
   }
 }
 
 template <int D>
-__device__ __forceinline__ void pack_unrotated(const half2_t (&x1)[Geo<D>::NP], const half2_t (&x2)[Geo<D>::NP],
-                                               half8_t (&ya)[Geo<D>::DS]) {
+__device__ __forceinline__ void rotate_he(const Half8s<Geo<D>::NV>& x1, const Half8s<Geo<D>::NV>& x2,
+                                          const Half8s<Geo<D>::NV>& c, const Half8s<Geo<D>::NV>& s,
+                                          half8_t (&ya)[Geo<D>::DS]) {
   using G = Geo<D>;
 #pragma unroll
-  for (int s = 0; s < G::DS; ++s) {
-    const half2_t* src = (s < G::DS / 2) ? &x1[4 * s] : &x2[4 * (s - G::DS / 2)];
-    ya[s] = (half8_t){src[0].x, src[0].y, src[1].x, src[1].y, src[2].x, src[2].y, src[3].x, src[3].y};
+  for (int v = 0; v < G::NV; ++v) {
+    ya[v] = c.v[v] * x1.v[v] - s.v[v] * x2.v[v];
+    ya[G::NV + v] = s.v[v] * x1.v[v] + c.v[v] * x2.v[v];
+  }
+}
+
+template <int D>
+__device__ __forceinline__ void unrotated(const Half8s<Geo<D>::NV>& x1, const Half8s<Geo<D>::NV>& x2,
+                                          half8_t (&ya)[Geo<D>::DS]) {
+  using G = Geo<D>;
+#pragma unroll
+  for (int v = 0; v < G::NV; ++v) {
+    ya[v] = x1.v[v];
+    ya[G::NV + v] = x2.v[v];
   }
 }
 
@@ -152,8 +179,9 @@ __device__ __forceinline__ void load_q(const DecodeParams& p, int b, int h, int 
   const h16* qrow = p.q + b * p.q_sb + (long)(h * p.nrep + (hv ? n : 0)) * p.q_sh;
 #pragma unroll
   for (int s = 0; s < G::DS; ++s) {
-    const int d0 = (s < G::DS / 2) ? g * G::QG + 8 * s : G::HALF + g * G::QG + 8 * (s - G::DS / 2);
-    qb[s] = hv ? *reinterpret_cast<const half8_t*>(qrow + d0) : (half8_t)(h16)0;
+    const int d0 = (s < G::NV) ? g * G::QG + 8 * s : G::HALF + g * G::QG + 8 * (s - G::NV);
+    const half8_t v = *reinterpret_cast<const half8_t*>(qrow + d0);
+    qb[s] = hv ? v : (half8_t)(h16)0;
   }
 }
 
@@ -171,151 +199,76 @@ __device__ __forceinline__ void write_empty(const DecodeParams& p, int b, int h,
 
 __device__ __forceinline__ int clamp_angle(int phi, int len) { return min(max(phi, 0), len - 1); }
 
-// ------------------------------------------------------------------ cold
-template <int D, int KK, int KV>
-__device__ void cold_unit(const DecodeParams& p, int b, int h, int j, float* lds) {
-  using G = Geo<D>;
-  const int lane = threadIdx.x & 63, w = threadIdx.x >> 6, g = lane >> 4, n = lane & 15;
-  const int ncold = p.counters[b * SC_NCOUNTERS + SC_CNT_NCOLD];
-  if (j >= ncold) {
-    write_empty(p, b, h, j, G::PREC);
-    return;
+// ds_swizzle bitmask mode: lane l reads lane (l & 0x30) | SRC of its 32-lane
+// half, i.e. lane SRC of its own 16-lane row.
+template <int SRC>
+__device__ __forceinline__ float row_bcast_c(float v) {
+  return __int_as_float(__builtin_amdgcn_ds_swizzle(__float_as_int(v), 0x10 | (SRC << 5)));
+}
+__device__ __forceinline__ float row_bcast(float v, int src) {
+  switch (src) {
+    case 0: return row_bcast_c<0>(v);
+    case 1: return row_bcast_c<1>(v);
+    case 2: return row_bcast_c<2>(v);
+    case 3: return row_bcast_c<3>(v);
+    case 4: return row_bcast_c<4>(v);
+    case 5: return row_bcast_c<5>(v);
+    case 6: return row_bcast_c<6>(v);
+    case 7: return row_bcast_c<7>(v);
+    case 8: return row_bcast_c<8>(v);
+    case 9: return row_bcast_c<9>(v);
+    case 10: return row_bcast_c<10>(v);
+    case 11: return row_bcast_c<11>(v);
+    case 12: return row_bcast_c<12>(v);
+    case 13: return row_bcast_c<13>(v);
+    case 14: return row_bcast_c<14>(v);
+    default: return row_bcast_c<15>(v);
   }
-  const int nrep = p.nrep;
-  const bool hv = n < nrep;
-  const long bhj = (long)(b * p.Hkv + h) * p.NB + j;
-  const int start = p.block_start[b * p.NB + j];
-  const int qp = p.qpos ? p.qpos[b] : p.qpos_scalar;
+}
 
-  half8_t qb[G::DS];
-  load_q<D>(p, b, h, g, n, hv, qb);
+// The reference rounds scores and logits to the model dtype (fp16) before
+// the fp32 softmax: s = fp16(raw) (kernels/spectral_attention.py:446,
+// spectral_attention.py:238), logits = fp16(s * scale) (:280-281).
+__device__ __forceinline__ h16 fp16_logit(float raw, float scale) {
+  return (h16)((float)(h16)raw * scale);
+}
 
-  // Basis of K as the A operand: row n of tile mt is d = perm(mt, n).
-  constexpr int KC = KK >= 32 ? KK / 32 : 1;
-  half8_t a8[G::MT][KC];
-  half4_t a4[G::MT];
-  const h16* bk = p.basis_k + bhj * (long)D * KK;
-#pragma unroll
-  for (int mt = 0; mt < G::MT; ++mt) {
-    const int hh = mt / G::MTH, mtl = mt % G::MTH;
-    const int d = hh * G::HALF + (n >> 2) * G::QG + 4 * mtl + (n & 3);
-    if constexpr (KK == 16) {
-      a4[mt] = *reinterpret_cast<const half4_t*>(bk + d * KK + 4 * g);
-    } else {
-#pragma unroll
-      for (int c = 0; c < KC; ++c) a8[mt][c] = *reinterpret_cast<const half8_t*>(bk + d * KK + c * 32 + 8 * g);
-    }
-  }
+__device__ __forceinline__ float fast_exp2(float x) { return __builtin_amdgcn_exp2f(x); }
 
-  const int8_t* ck = p.codes_k + bhj * (long)p.TB * KK;
-  const int8_t* cv = p.codes_v + bhj * (long)KV * p.TB;
-  const float* skp = p.scales_k + (p.per_row ? bhj * p.TB : bhj);
-  const float* svp = p.scales_v + (p.per_row ? bhj * p.TB : bhj);
-  const float vn = p.vnorm[bhj];
-  const int kind = p.rope_mode == SC_ROPE_DISTANCE ? kRotDist : kRotColdAbs;
-  const uint8_t* mrow = (p.mask && hv) ? p.mask + b * p.mask_sb + (long)(h * nrep + n) * p.mask_sh + (long)j * p.TB : nullptr;
-  float* lrow = (p.logits && hv) ? p.logits + b * p.lg_sb + (long)(h * nrep + n) * p.lg_sh + (long)j * p.TB : nullptr;
+// Maximum of a lane's logits (fp16, four per tile) in the log2 domain.
+template <int NTILE>
+__device__ __forceinline__ float lane_max_log2(const half4_t (&lg)[NTILE]) {
+  half4_t m = lg[0];
+#pragma unroll
+  for (int i = 1; i < NTILE; ++i) m = __builtin_elementwise_max(m, lg[i]);
+  const float a = fmaxf((float)m[0], (float)m[1]), c = fmaxf((float)m[2], (float)m[3]);
+  return fmaxf(a, c) * kLog2e;
+}
 
-  float m_run = -INFINITY, l_run = 0.f;
-  float4_t pacc[KV / 16];
-#pragma unroll
-  for (int nt = 0; nt < KV / 16; ++nt) pacc[nt] = (float4_t)0.f;
-
-  const int per_wave = p.TB / kWaves;
-  const int tok0 = w * per_wave;
-  for (int tb = tok0; tb < tok0 + per_wave; tb += kTile) {
-    // 1. reconstruct X^T[d][token] for the 16 tokens of the tile.
-    float4_t x[G::MT];
-    if constexpr (KK == 16) {
-      const half4_t bc = i8x4_to_h4(*reinterpret_cast<const uint32_t*>(ck + (tb + n) * KK + 4 * g));
-#pragma unroll
-      for (int mt = 0; mt < G::MT; ++mt) x[mt] = mfma_16x16x16(a4[mt], bc, (float4_t)0.f);
-    } else {
-      half8_t bc[KC];
-#pragma unroll
-      for (int c = 0; c < KC; ++c)
-        bc[c] = i8x8_to_h8(*reinterpret_cast<const uint2*>(ck + (tb + n) * KK + c * 32 + 8 * g));
-#pragma unroll
-      for (int mt = 0; mt < G::MT; ++mt) {
-        float4_t acc = (float4_t)0.f;
-#pragma unroll
-        for (int c = 0; c < KC; ++c) acc = mfma_16x16x32(a8[mt][c], bc[c], acc);
-        x[mt] = acc;
-      }
-    }
-    half2_t x1[G::NP], x2[G::NP];
-#pragma unroll
-    for (int e = 0; e < G::NP; ++e) {
-      const int mt = (2 * e) >> 2, jj = (2 * e) & 3;
-      x1[e] = pack_h2(x[mt][jj], x[mt][jj + 1]);
-      x2[e] = pack_h2(x[G::MTH + mt][jj], x[G::MTH + mt][jj + 1]);
-    }
-    // 2. RoPE of token tb + n.
-    half8_t ya[G::DS];
-    if (p.rope_mode == SC_ROPE_NONE) {
-      pack_unrotated<D>(x1, x2, ya);
-    } else {
-      const int pos = start + tb + n;
-      const int phi = clamp_angle(p.rope_mode == SC_ROPE_DISTANCE ? max(qp - pos, 0) : pos, p.rope_len);
-      rotate_pairs<D>(x1, x2, p.cos + phi * p.rope_stride, p.sin + phi * p.rope_stride, g, kind,
-                      p.halves_equal != 0, ya);
-    }
-    // 3. scores of the GQA group: lane holds head n, tokens tb + 4g + jj.
-    float4_t sacc = (float4_t)0.f;
-#pragma unroll
-    for (int s = 0; s < G::DS; ++s) sacc = mfma_16x16x32(ya[s], qb[s], sacc);
-    const float4_t sk4 = p.per_row ? *reinterpret_cast<const float4_t*>(skp + tb + 4 * g) : (float4_t)skp[0];
-    float sc[4];
-    uint32_t keep = 0xffffffffu;
-    if (mrow) keep = *reinterpret_cast<const uint32_t*>(mrow + tb + 4 * g);
-#pragma unroll
-    for (int jj = 0; jj < 4; ++jj) {
-      const float raw = sacc[jj] * sk4[jj];
-      if (lrow) lrow[tb + 4 * g + jj] = raw * p.scale;
-      const bool k = hv && ((keep >> (8 * jj)) & 0xffu);
-      sc[jj] = k ? raw * p.scale_log2 : -INFINITY;
-    }
-    // 4. online softmax (log2 domain).
-    const float tmax = max_over_rows(fmaxf(fmaxf(sc[0], sc[1]), fmaxf(sc[2], sc[3])));
-    const float m_new = fmaxf(m_run, tmax);
-    const bool live = m_new != -INFINITY;
-    const float alpha = live ? exp2f(m_run - m_new) : 1.f;
-    float pv[4];
-#pragma unroll
-    for (int jj = 0; jj < 4; ++jj) pv[jj] = live ? exp2f(sc[jj] - m_new) : 0.f;
-    l_run = l_run * alpha + sum_over_rows(pv[0] + pv[1] + pv[2] + pv[3]);
-    m_run = m_new;
-    // 5. Pacc^T[i][head] += C_V^T[i][tok] . (P s_V vnorm)[tok][head]
-    const float4_t sv4 = p.per_row ? *reinterpret_cast<const float4_t*>(svp + tb + 4 * g) : (float4_t)svp[0];
-    const half4_t pb = {(h16)(pv[0] * sv4[0] * vn), (h16)(pv[1] * sv4[1] * vn), (h16)(pv[2] * sv4[2] * vn),
-                        (h16)(pv[3] * sv4[3] * vn)};
-#pragma unroll
-    for (int nt = 0; nt < KV / 16; ++nt) {
-      const half4_t ca = i8x4_to_h4(*reinterpret_cast<const uint32_t*>(cv + (long)(nt * 16 + n) * p.TB + tb + 4 * g));
-      pacc[nt] = mfma_16x16x16(ca, pb, pacc[nt] * alpha);
-    }
-  }
-
-  // ---- merge the four waves, project through B_V once.
-  float* s_m = lds;                         // [kWaves][nrep]
-  float* s_l = s_m + kWaves * nrep;         // [kWaves][nrep]
-  float* s_acc = s_l + kWaves * nrep;       // [kWaves][nrep][KV]
-  float* s_mrg = s_acc + kWaves * nrep * KV;  // [nrep][KV]
-  float* s_ml = s_mrg + nrep * KV;          // [nrep][2]
+// Merges the four waves' (m, l, acc[W]) in LDS.  Leaves the merged
+// accumulators in s_mrg[nrep][W] (scaled by post) and (M, L) in s_ml.
+template <int W>
+__device__ __forceinline__ void merge_waves(float* lds, int nrep, int w, int g, int n, bool hv, float m_run,
+                                            float l_run, const float* accv, float post, float*& s_mrg,
+                                            float*& s_ml) {
+  float* s_m = lds;                    // [kWaves][nrep]
+  float* s_l = s_m + kWaves * nrep;    // [kWaves][nrep]
+  float* s_acc = s_l + kWaves * nrep;  // [kWaves][nrep][W]
+  s_mrg = s_acc + kWaves * nrep * W;   // [nrep][W]
+  s_ml = s_mrg + nrep * W;             // [nrep][2]
   if (hv) {
     if (g == 0) {
       s_m[w * nrep + n] = m_run;
       s_l[w * nrep + n] = l_run;
     }
 #pragma unroll
-    for (int nt = 0; nt < KV / 16; ++nt)
+    for (int t = 0; t < W / 16; ++t)
 #pragma unroll
-      for (int jj = 0; jj < 4; ++jj) s_acc[(w * nrep + n) * KV + nt * 16 + 4 * g + jj] = pacc[nt][jj];
+      for (int jj = 0; jj < 4; ++jj) s_acc[(w * nrep + n) * W + t * 16 + 4 * g + jj] = accv[4 * t + jj];
   }
   __syncthreads();
-  const float inv_vn = 1.0f / vn;
-  for (int idx = threadIdx.x; idx < nrep * KV; idx += kThreads) {
-    const int hh = idx / KV, i = idx % KV;
+  for (int idx = threadIdx.x; idx < nrep * W; idx += kThreads) {
+    const int hh = idx / W, i = idx % W;
     float M = -INFINITY;
 #pragma unroll
     for (int ww = 0; ww < kWaves; ++ww) M = fmaxf(M, s_m[ww * nrep + hh]);
@@ -324,192 +277,706 @@ __device__ void cold_unit(const DecodeParams& p, int b, int h, int j, float* lds
 #pragma unroll
       for (int ww = 0; ww < kWaves; ++ww) {
         const float mw = s_m[ww * nrep + hh];
-        const float a = (mw == -INFINITY) ? 0.f : exp2f(mw - M);
-        acc += a * s_acc[(ww * nrep + hh) * KV + i];
+        const float a = (mw == -INFINITY) ? 0.f : fast_exp2(mw - M);
+        acc += a * s_acc[(ww * nrep + hh) * W + i];
         L += a * s_l[ww * nrep + hh];
       }
     }
-    s_mrg[idx] = acc * inv_vn;
+    s_mrg[idx] = acc * post;
     if (i == 0) {
       s_ml[2 * hh] = M;
       s_ml[2 * hh + 1] = L;
     }
   }
   __syncthreads();
-  const h16* bv = p.basis_v + bhj * (long)KV * D;
-  for (int idx = threadIdx.x; idx < nrep * D; idx += kThreads) {
-    const int hh = idx / D, d = idx % D;
-    float o = 0.f;
-#pragma unroll 8
-    for (int i = 0; i < KV; ++i) o += s_mrg[hh * KV + i] * (float)bv[i * D + d];
-    record_ptr(p, b, h, j, hh, G::PREC)[2 + d] = o;
+}
+
+// ------------------------------------------------------------------ cold
+// Staged RoPE rows.  LDS row rho of a range holds the cos/sin entries of
+// range token swap(rho) (bit fields [2:3] and [4:5] exchanged): the 16
+// lanes of a score tile then read 16 consecutive rows, and a row pitch of
+// an odd number of 16-byte chunks keeps those reads free of bank conflicts.
+__device__ __forceinline__ int swap_fields(int r) { return (r & ~0x3c) | ((r & 0x0c) << 2) | ((r & 0x30) >> 2); }
+
+template <int D, bool HE>
+struct RopeStage {
+  static constexpr int HCH = D / 16;                 // 16-byte chunks per half row of one table
+  static constexpr int CH = HE ? 2 * HCH : 4 * HCH;  // cos1 | sin1 (| cos2 | sin2)
+  static constexpr int ROW = CH * 16 + 16;           // LDS row pitch in bytes
+};
+
+// Chunk k of this thread's share of a range's RoPE rows: global source and
+// LDS destination.
+template <int D, bool HE>
+struct StageChunk {
+  const uint4* src;
+  int dst;
+};
+template <int D, bool HE>
+__device__ __forceinline__ StageChunk<D, HE> stage_chunk(const DecodeParams& p, int k, int pos0, int qp, bool dist) {
+  using RS = RopeStage<D, HE>;
+  const int c = k * kThreads + threadIdx.x;
+  const int r = c / RS::CH, q = c % RS::CH;
+  const int pos = pos0 + swap_fields(r);
+  const int phi = clamp_angle(dist ? max(qp - pos, 0) : pos, p.rope_len);
+  const int half = q / (2 * RS::HCH), qq = q % (2 * RS::HCH);
+  const h16* tab = qq < RS::HCH ? p.cos : p.sin;
+  StageChunk<D, HE> s;
+  s.src = reinterpret_cast<const uint4*>(tab + (long)phi * p.rope_stride + half * (D / 2) + 8 * (qq % RS::HCH));
+  s.dst = r * RS::ROW + q * 16;
+  return s;
+}
+
+template <int D, bool HE>
+__device__ __forceinline__ Half8s<Geo<D>::NV> lds_rope(const char* smem, int row, int chunk) {
+  Half8s<Geo<D>::NV> r;
+#pragma unroll
+  for (int v = 0; v < Geo<D>::NV; ++v)
+    r.v[v] = *reinterpret_cast<const half8_t*>(smem + row * RopeStage<D, HE>::ROW + (chunk + v) * 16);
+  return r;
+}
+
+// INT8 codes and scales of one wave's range (16 TPW tokens of one head).
+// sk[i] / sv[i]: the row scales of the four tokens a lane's score slots
+// hold in tile i (one 16-byte load per lane; the 16 lanes of a row share it).
+template <int KK, int KV, int TPW>
+struct CodeBuf {
+  static constexpr int NGRP = TPW / 4, NT = KV / 16, KC = KK >= 32 ? KK / 32 : 1;
+  using CodeK = typename std::conditional<KK == 16, uint32_t, uint2>::type;
+  CodeK kc[TPW][KC];
+  uint4 vc[NGRP][NT];
+  float4_t sk[TPW], sv[TPW];
+};
+
+// Loads of one wave's codes (range starting at block token tok0).  Each
+// part can be issued on its own so that a register is refilled with the
+// next range's data right after its last use.
+template <int KK, int KV, int TPW>
+struct CodeSrc {
+  const int8_t* ck;   // K codes of the range
+  const int8_t* cv;   // V codes of the range
+  const float* skp;   // K scales (per row: the range's first token; per head: the value)
+  const float* svp;
+};
+
+template <int KK, int KV, int TPW>
+__device__ __forceinline__ CodeSrc<KK, KV, TPW> code_src(const DecodeParams& p, long bhj, int tok0) {
+  CodeSrc<KK, KV, TPW> s;
+  s.ck = p.codes_k + bhj * (long)p.TB * KK + (long)tok0 * KK;
+  s.cv = p.codes_v + bhj * (long)KV * p.TB + tok0;
+  s.skp = p.scales_k + (p.per_row ? bhj * p.TB + tok0 : bhj);
+  s.svp = p.scales_v + (p.per_row ? bhj * p.TB + tok0 : bhj);
+  return s;
+}
+
+template <int KK, int KV, int TPW>
+__device__ __forceinline__ void load_kc(const CodeSrc<KK, KV, TPW>& s, int i, CodeBuf<KK, KV, TPW>& cb) {
+  using CB = CodeBuf<KK, KV, TPW>;
+  const int lane = threadIdx.x & 63, g = lane >> 4, n = lane & 15;
+  const int tt = (i / 4) * 64 + 16 * (n >> 2) + 4 * (i % 4) + (n & 3);
+#pragma unroll
+  for (int c = 0; c < CB::KC; ++c) {
+    if constexpr (KK == 16)
+      cb.kc[i][c] = *reinterpret_cast<const uint32_t*>(s.ck + tt * KK + 4 * g);
+    else
+      cb.kc[i][c] = *reinterpret_cast<const uint2*>(s.ck + tt * KK + c * 32 + 8 * g);
   }
-  if ((int)threadIdx.x < nrep) {
-    float* r = record_ptr(p, b, h, j, threadIdx.x, G::PREC);
-    r[0] = s_ml[2 * threadIdx.x];
-    r[1] = s_ml[2 * threadIdx.x + 1];
+}
+
+template <int KK, int KV, int TPW>
+__device__ __forceinline__ void load_vc(const DecodeParams& p, const CodeSrc<KK, KV, TPW>& s, int gr,
+                                        CodeBuf<KK, KV, TPW>& cb) {
+  using CB = CodeBuf<KK, KV, TPW>;
+  const int lane = threadIdx.x & 63, g = lane >> 4, n = lane & 15;
+#pragma unroll
+  for (int nt = 0; nt < CB::NT; ++nt)
+    cb.vc[gr][nt] = *reinterpret_cast<const uint4*>(s.cv + (long)(nt * 16 + n) * p.TB + gr * 64 + 16 * g);
+}
+
+// Row scales of tokens 64 (i / 4) + 16 g + 4 (i % 4) + {0..3} of the range
+// (per row), or the block's scale four times (per head).
+__device__ __forceinline__ float4_t load_scale4(const DecodeParams& p, const float* base, int i) {
+  const int g = (threadIdx.x & 63) >> 4;
+  if (p.per_row) return *reinterpret_cast<const float4_t*>(base + 64 * (i / 4) + 16 * g + 4 * (i % 4));
+  return (float4_t)base[0];
+}
+
+template <int KK, int KV, int TPW>
+__device__ __forceinline__ void load_codes(const DecodeParams& p, const CodeSrc<KK, KV, TPW>& s,
+                                           CodeBuf<KK, KV, TPW>& cb) {
+  using CB = CodeBuf<KK, KV, TPW>;
+#pragma unroll
+  for (int i = 0; i < TPW; ++i) load_kc<KK, KV, TPW>(s, i, cb);
+#pragma unroll
+  for (int gr = 0; gr < CB::NGRP; ++gr) load_vc<KK, KV, TPW>(p, s, gr, cb);
+#pragma unroll
+  for (int i = 0; i < TPW; ++i) {
+    cb.sk[i] = load_scale4(p, s.skp, i);
+    cb.sv[i] = load_scale4(p, s.svp, i);
+  }
+}
+
+// Running state of one wave (one KV head) across the ranges of a block.
+template <int KV>
+struct ColdState {
+  float m2, l;  // running max (log2 domain, per head = lane column) and lane-partial sum
+  float4_t pacc[KV / 16];
+};
+
+// Scores (phase A), one maximum (B), probabilities and P . C_V (C) of one
+// range, merged into the running state.  The RoPE rows of the next range
+// (if any) are fetched into registers before phase A and written to the
+// other LDS buffer after it; every code register is refilled with the next
+// range's data (nsrc, if any) right after its last use, so the next range's
+// HBM loads are in flight during this one.
+template <int D, int KK, int KV, int TPW, bool GEN, bool HE>
+__device__ __forceinline__ void cold_range(const DecodeParams& p, CodeBuf<KK, KV, TPW>& cb,
+                                           const CodeSrc<KK, KV, TPW> nsrc, bool reload,
+                                           const half8_t (&a8)[Geo<D>::MT][CodeBuf<KK, KV, TPW>::KC],
+                                           const half4_t (&a4)[Geo<D>::MT], const half8_t (&qb)[Geo<D>::DS],
+                                           const char* rope_cur, char* rope_next, int next_pos0, int qp, bool dist,
+                                           bool rope, float vn, const uint8_t* mrow, float* lrow,
+                                           ColdState<KV>& st) {
+  using G = Geo<D>;
+  using CB = CodeBuf<KK, KV, TPW>;
+  using RS = RopeStage<D, HE>;
+  constexpr int NSTG = (TPW * kTile) * RS::CH / kThreads;  // staged chunks per thread
+  const int lane = threadIdx.x & 63, g = lane >> 4, n = lane & 15;
+  const bool stage = rope && rope_next != nullptr;
+  // The next range's RoPE rows (L2 hits) are requested before any of this
+  // range's HBM refills: vmcnt retires in order, so waiting for them before
+  // the LDS stores below never waits for the refills.
+  // (Loaded whenever the tables exist: past the last range the angles are
+  // clamped into the table, and only the stores below are skipped.)
+  uint4 sv[NSTG];
+  int sd[NSTG];
+#pragma unroll
+  for (int k = 0; k < NSTG; ++k) {
+    const StageChunk<D, HE> sc = stage_chunk<D, HE>(p, k, next_pos0, qp, dist);
+    sv[k] = rope ? *sc.src : uint4{0, 0, 0, 0};
+    sd[k] = sc.dst;
+  }
+  half4_t lg[TPW];
+#pragma unroll
+  for (int i = 0; i < TPW; ++i) {
+    const int gr = i / 4, ii = i % 4;
+    float4_t x[G::MT];
+    if constexpr (KK == 16) {
+      const half4_t bc = i8x4_to_h4(cb.kc[i][0]);
+      if (reload) load_kc<KK, KV, TPW>(nsrc, i, cb);
+#pragma unroll
+      for (int mt = 0; mt < G::MT; ++mt) x[mt] = mfma_16x16x16(a4[mt], bc, (float4_t)0.f);
+    } else {
+      half8_t bc[CB::KC];
+#pragma unroll
+      for (int c = 0; c < CB::KC; ++c) bc[c] = i8x8_to_h8(cb.kc[i][c]);
+      if (reload) load_kc<KK, KV, TPW>(nsrc, i, cb);
+#pragma unroll
+      for (int mt = 0; mt < G::MT; ++mt) {
+        float4_t acc = (float4_t)0.f;
+#pragma unroll
+        for (int c = 0; c < CB::KC; ++c) acc = mfma_16x16x32(a8[mt][c], bc[c], acc);
+        x[mt] = acc;
+      }
+    }
+    Half8s<G::NV> x1, x2;
+    pack_x<D>(x, x1, x2);
+    const int row = gr * 64 + 16 * ii + n;  // staged row of this lane's token
+    half8_t ya[G::DS];
+    if constexpr (!GEN) {
+      rotate_he<D>(x1, x2, lds_rope<D, true>(rope_cur, row, g * G::NV),
+                   lds_rope<D, true>(rope_cur, row, RS::HCH + g * G::NV), ya);
+    } else {
+      if (!rope) {
+        unrotated<D>(x1, x2, ya);
+      } else if constexpr (HE) {
+        rotate_he<D>(x1, x2, lds_rope<D, true>(rope_cur, row, g * G::NV),
+                     lds_rope<D, true>(rope_cur, row, RS::HCH + g * G::NV), ya);
+      } else {
+        rotate<D>(x1, x2, lds_rope<D, false>(rope_cur, row, g * G::NV),
+                  lds_rope<D, false>(rope_cur, row, RS::HCH + g * G::NV),
+                  lds_rope<D, false>(rope_cur, row, 2 * RS::HCH + g * G::NV),
+                  lds_rope<D, false>(rope_cur, row, 3 * RS::HCH + g * G::NV), dist ? kRotDist : kRotColdAbs, ya);
+      }
+    }
+    float4_t sacc = (float4_t)0.f;
+#pragma unroll
+    for (int s = 0; s < G::DS; ++s) sacc = mfma_16x16x32(ya[s], qb[s], sacc);
+    // lane holds head n, range tokens tg + jj, tg = 64 gr + 16 g + 4 ii
+    const int tg = gr * 64 + 16 * g + 4 * ii;
+#pragma unroll
+    for (int jj = 0; jj < 4; ++jj) lg[i][jj] = fp16_logit(sacc[jj] * cb.sk[i][jj], p.scale);
+    if (reload) cb.sk[i] = load_scale4(p, nsrc.skp, i);
+    if constexpr (GEN) {
+      uint32_t keep = 0xffffffffu;
+      if (mrow) keep = *reinterpret_cast<const uint32_t*>(mrow + tg);
+#pragma unroll
+      for (int jj = 0; jj < 4; ++jj) {
+        if (lrow) lrow[tg + jj] = (float)lg[i][jj];
+        if (!((keep >> (8 * jj)) & 0xffu)) lg[i][jj] = (h16)(-INFINITY);
+      }
+    }
+  }
+  if (stage) {
+#pragma unroll
+    for (int k = 0; k < NSTG; ++k) *reinterpret_cast<uint4*>(rope_next + sd[k]) = sv[k];
+  }
+  // ---- B. range maximum, merged into the running maximum
+  const float mr = max_over_rows(lane_max_log2<TPW>(lg));
+  const float m_new = fmaxf(st.m2, mr);
+  const float msub = (m_new == -INFINITY) ? 0.f : m_new;
+  const float alpha = fast_exp2(st.m2 - msub);  // exp2(-inf) = 0 on the first range
+  st.m2 = m_new;
+  st.l *= alpha;
+  // ---- C. probabilities and P . C_V
+#pragma unroll
+  for (int nt = 0; nt < CB::NT; ++nt) st.pacc[nt] *= alpha;
+#pragma unroll
+  for (int i = 0; i < TPW; ++i) {
+    const int gr = i / 4, ii = i % 4;
+    float pv[4];
+#pragma unroll
+    for (int jj = 0; jj < 4; ++jj) {
+      pv[jj] = fast_exp2(__builtin_fmaf((float)lg[i][jj], kLog2e, -msub));
+      st.l += pv[jj];
+    }
+    const float4_t svn = cb.sv[i] * vn;
+    const half4_t pb = {(h16)(pv[0] * svn[0]), (h16)(pv[1] * svn[1]), (h16)(pv[2] * svn[2]), (h16)(pv[3] * svn[3])};
+    if (reload) cb.sv[i] = load_scale4(p, nsrc.svp, i);
+#pragma unroll
+    for (int nt = 0; nt < CB::NT; ++nt) {
+      const uint4 w4 = cb.vc[gr][nt];
+      const uint32_t word = ii == 0 ? w4.x : ii == 1 ? w4.y : ii == 2 ? w4.z : w4.w;
+      st.pacc[nt] = mfma_16x16x16(i8x4_to_h4(word), pb, st.pacc[nt]);
+    }
+    if (ii == 3 && reload) load_vc<KK, KV, TPW>(p, nsrc, gr, cb);
+  }
+}
+
+// Cold unit: one workgroup per (sequence b, cold block j, group of four KV
+// heads); wave w is KV head 4 hq + w.  The block is walked in ranges of
+// T = 16 TPW tokens; the RoPE rows of a range are staged once per
+// workgroup in LDS (double-buffered) and the INT8 codes of the next range
+// are in flight (ping-pong register buffers) while the current one is
+// processed.  Each wave writes one partial record per block.
+template <int D, int KK, int KV, int TPW, bool GEN, bool HE>
+__device__ void cold_unit(const DecodeParams& p, int b, int hq, int j, char* smem) {
+  using G = Geo<D>;
+  using CB = CodeBuf<KK, KV, TPW>;
+  using RS = RopeStage<D, HE>;
+  constexpr int T = kTile * TPW;
+  constexpr int NT = KV / 16;
+  constexpr int KC = CB::KC;
+  const int lane = threadIdx.x & 63, w = threadIdx.x >> 6, g = lane >> 4, n = lane & 15;
+  const int h = hq * kWaves + w;
+  const bool hvalid = h < p.Hkv;
+  const int ncold = p.counters[b * SC_NCOUNTERS + SC_CNT_NCOLD];
+  if (j >= ncold) {  // uniform over the workgroup
+    if (hvalid && lane < p.nrep) {
+      float* r = record_ptr(p, b, h, j, lane, G::PREC);
+      r[0] = -INFINITY;
+      r[1] = 0.f;
+    }
+    return;
+  }
+  const int nrep = p.nrep;
+  const bool hv = n < nrep;
+  const long bhj = (long)(b * p.Hkv + (hvalid ? h : 0)) * p.NB + j;
+  const int start = p.block_start[b * p.NB + j];
+  const int qp = p.qpos ? p.qpos[b] : p.qpos_scalar;
+  const bool dist = p.rope_mode == SC_ROPE_DISTANCE;
+  const bool rope = !GEN || p.rope_mode != SC_ROPE_NONE;
+  const int R = p.TB / T;  // ranges per block
+  constexpr int RBUF = T * RS::ROW;  // bytes of one staged range
+
+  // ---- prologue: RoPE rows of range 0 (L2) first, then the HBM loads
+  constexpr int NSTG = T * RS::CH / kThreads;
+  if (rope) {
+    uint4 v[NSTG];
+    int dst[NSTG];
+#pragma unroll
+    for (int k = 0; k < NSTG; ++k) {
+      const StageChunk<D, HE> s = stage_chunk<D, HE>(p, k, start, qp, dist);
+      v[k] = *s.src;
+      dst[k] = s.dst;
+    }
+#pragma unroll
+    for (int k = 0; k < NSTG; ++k) *reinterpret_cast<uint4*>(smem + dst[k]) = v[k];
+  }
+  // Codes of DEPTH consecutive ranges are in flight: two for ranks up to
+  // 32, one for larger ranks (register budget).
+  constexpr int DEPTH = 1;
+  CB cb0, cb1;
+  half8_t a8[G::MT][KC];
+  half4_t a4[G::MT];
+  half8_t qb[G::DS];
+  float vn = 1.f;
+  if (hvalid) {
+    load_codes<KK, KV, TPW>(p, code_src<KK, KV, TPW>(p, bhj, 0), cb0);
+    if (DEPTH == 2 && R > 1) load_codes<KK, KV, TPW>(p, code_src<KK, KV, TPW>(p, bhj, T), cb1);
+    // K basis as the A operand: row n of tile mt is d = perm(mt, n).
+    const h16* bk = p.basis_k + bhj * (long)D * KK;
+#pragma unroll
+    for (int mt = 0; mt < G::MT; ++mt) {
+      const int hh = mt / G::MTH, mtl = mt % G::MTH;
+      const int d = hh * G::HALF + (n >> 2) * G::QG + 4 * mtl + (n & 3);
+      if constexpr (KK == 16) {
+        a4[mt] = *reinterpret_cast<const half4_t*>(bk + d * KK + 4 * g);
+      } else {
+#pragma unroll
+        for (int c = 0; c < KC; ++c) a8[mt][c] = *reinterpret_cast<const half8_t*>(bk + d * KK + c * 32 + 8 * g);
+      }
+    }
+    if (hv) {
+      load_q<D>(p, b, h, g, n, true, qb);
+    } else {
+#pragma unroll
+      for (int s = 0; s < G::DS; ++s) qb[s] = (half8_t)(h16)0;
+    }
+    vn = p.vnorm[bhj];
+  }
+  const long cache_tok = (long)j * p.TB;  // cache-order index of the block's first token
+  const uint8_t* mrow = nullptr;
+  float* lrow = nullptr;
+  if constexpr (GEN) {
+    mrow = (p.mask && hv) ? p.mask + b * p.mask_sb + (long)(h * nrep + n) * p.mask_sh + cache_tok : nullptr;
+    lrow = (p.logits && hv) ? p.logits + b * p.lg_sb + (long)(h * nrep + n) * p.lg_sh + cache_tok : nullptr;
+  }
+  ColdState<KV> st;
+  st.m2 = -INFINITY;
+  st.l = 0.f;
+#pragma unroll
+  for (int nt = 0; nt < NT; ++nt) st.pacc[nt] = (float4_t)0.f;
+  __syncthreads();
+
+  // ---- ranges: range rr uses cb0 / cb1 by parity (DEPTH 2) or cb0, and
+  // refills it with range rr + DEPTH right after each register's last use.
+  auto range = [&](int rr, CB& cb) {
+    const bool more = rr + 1 < R;
+    char* cur = smem + (rr & 1) * RBUF;
+    char* next = more ? smem + ((rr + 1) & 1) * RBUF : nullptr;
+    if (hvalid) {
+      cold_range<D, KK, KV, TPW, GEN, HE>(p, cb, code_src<KK, KV, TPW>(p, bhj, (rr + DEPTH) * T), rr + DEPTH < R, a8, a4,
+                                          qb, cur, next, start + (rr + 1) * T, qp, dist, rope, vn,
+                                          mrow ? mrow + rr * T : nullptr, lrow ? lrow + rr * T : nullptr, st);
+    } else if (rope && more) {
+      // idle head slot: still stage its share of the next range's rows
+      uint4 v[NSTG];
+      int dst[NSTG];
+#pragma unroll
+      for (int k = 0; k < NSTG; ++k) {
+        const StageChunk<D, HE> s = stage_chunk<D, HE>(p, k, start + (rr + 1) * T, qp, dist);
+        v[k] = *s.src;
+        dst[k] = s.dst;
+      }
+#pragma unroll
+      for (int k = 0; k < NSTG; ++k) *reinterpret_cast<uint4*>(next + dst[k]) = v[k];
+    }
+    __syncthreads();
+  };
+  if constexpr (DEPTH == 2) {
+    for (int rr = 0; rr < R; rr += 2) {
+      range(rr, cb0);
+      if (rr + 1 < R) range(rr + 1, cb1);
+    }
+  } else {
+    for (int rr = 0; rr < R; ++rr) range(rr, cb0);
+  }
+  if (!hvalid) return;
+  st.l = sum_over_rows(st.l);
+
+  // ---- projection O^T[d][head] = B_V^T[d][i] . Pacc[i][head] on MFMA; Pacc
+  // (coefficient i = 16 nt + 4 g + jj of head n, already the B-operand
+  // layout) is split into fp16 hi + lo parts to keep fp32 accuracy.
+  half4_t bvf[G::MT][NT];
+  const h16* bvb = p.basis_v + bhj * (long)D * KV;
+#pragma unroll
+  for (int mt = 0; mt < G::MT; ++mt)
+#pragma unroll
+    for (int nt = 0; nt < NT; ++nt)
+      bvf[mt][nt] = *reinterpret_cast<const half4_t*>(bvb + (long)(16 * mt + n) * KV + 16 * nt + 4 * g);
+  half4_t ph[NT], pl[NT];
+#pragma unroll
+  for (int nt = 0; nt < NT; ++nt)
+#pragma unroll
+    for (int jj = 0; jj < 4; ++jj) {
+      const h16 hi = (h16)st.pacc[nt][jj];
+      ph[nt][jj] = hi;
+      pl[nt][jj] = (h16)(st.pacc[nt][jj] - (float)hi);
+    }
+  const float ivn = 1.0f / vn;
+  float* rec = record_ptr(p, b, h, j, hv ? n : 0, G::PREC);
+#pragma unroll
+  for (int mt = 0; mt < G::MT; ++mt) {
+    float4_t o = (float4_t)0.f;
+#pragma unroll
+    for (int nt = 0; nt < NT; ++nt) {
+      o = mfma_16x16x16(bvf[mt][nt], ph[nt], o);
+      o = mfma_16x16x16(bvf[mt][nt], pl[nt], o);
+    }
+    if (hv) *reinterpret_cast<float4_t*>(rec + 4 + 16 * mt + 4 * g) = o * ivn;
+  }
+  if (hv && g == 0) {
+    rec[0] = st.m2;
+    rec[1] = st.l;
   }
 }
 
 // ------------------------------------------------------------------ tail
-template <int D>
+template <int D, bool GEN>
 __device__ void tail_unit(const DecodeParams& p, int b, int h, int c, float* lds) {
   using G = Geo<D>;
+  constexpr int QPR = D / 32;  // 16-byte chunks per quarter of a staged V row
   const int lane = threadIdx.x & 63, w = threadIdx.x >> 6, g = lane >> 4, n = lane & 15;
-  const int unit = p.grid_blocks + c;
+  const int unit = p.cold_units + c;
   const int* cnt = p.counters + b * SC_NCOUNTERS;
   const int tl = cnt[SC_CNT_TAIL_LEN], th = cnt[SC_CNT_TAIL_HEAD], ncold = cnt[SC_CNT_NCOLD];
-  if (c * kTailUnit >= tl) {
+  if (c * kTailUnit >= tl) {  // uniform over the workgroup
     write_empty(p, b, h, unit, G::PREC);
     return;
   }
   const int nrep = p.nrep;
   const bool hv = n < nrep;
   const long bh = (long)(b * p.Hkv + h);
-  const int tile0 = c * kTailUnit + w * kTile;
+  const int wtok0 = c * kTailUnit + w * (kTailTiles * kTile);  // first tail token of the wave
 
+  // ---- issue loads: key rows (lane n = token), positions, V quarter rows
+  Half8s<G::NV> kx1[kTailTiles], kx2[kTailTiles];
+  int kpos[kTailTiles];
+  half8_t vq[kTailTiles][QPR];
+  const int vr = lane >> 2, vqtr = lane & 3;
+#pragma unroll
+  for (int i = 0; i < kTailTiles; ++i) {
+    const int t = wtok0 + i * kTile + n;
+    const bool tv = t < tl;
+    const int slot = (th + (tv ? t : 0)) % p.TCAP;
+    const h16* krow = p.tail_k + (bh * p.TCAP + slot) * D + g * G::QG;
+    kx1[i] = load_h8s<G::NV>(krow);
+    kx2[i] = load_h8s<G::NV>(krow + G::HALF);
+    kpos[i] = p.tail_pos[(long)b * p.TCAP + slot];
+    if (!tv) {
+#pragma unroll
+      for (int v = 0; v < G::NV; ++v) kx1[i].v[v] = kx2[i].v[v] = (half8_t)(h16)0;
+    }
+    const int t2 = wtok0 + i * kTile + vr;
+    const bool vv = t2 < tl;
+    const int vslot = (th + (vv ? t2 : 0)) % p.TCAP;
+    const h16* vrow = p.tail_v + (bh * p.TCAP + vslot) * D + vqtr * (D / 4);
+#pragma unroll
+    for (int q = 0; q < QPR; ++q) {
+      const half8_t v = *reinterpret_cast<const half8_t*>(vrow + 8 * q);
+      vq[i][q] = vv ? v : (half8_t)(h16)0;
+    }
+  }
   half8_t qb[G::DS];
   load_q<D>(p, b, h, g, n, hv, qb);
-
-  // Key row of token tile0 + n.
-  const int t = tile0 + n;
-  const bool tv = t < tl;
-  const int slot = (th + (tv ? t : 0)) % p.TCAP;
-  half2_t x1[G::NP], x2[G::NP];
-  if (tv) {
-    const h16* krow = p.tail_k + (bh * p.TCAP + slot) * D;
-    load_pairs<G::QG>(krow + g * G::QG, x1);
-    load_pairs<G::QG>(krow + G::HALF + g * G::QG, x2);
-  } else {
+  const bool rope = !GEN || p.rope_mode != SC_ROPE_NONE;
+  const bool he = !GEN || p.halves_equal != 0;
+  const int kind = p.rope_mode == SC_ROPE_DISTANCE ? kRotDist : kRotTailAbs;
+  Half8s<G::NV> rc[kTailTiles], rs[kTailTiles];
+  if (rope) {
 #pragma unroll
-    for (int e = 0; e < G::NP; ++e) x1[e] = x2[e] = (half2_t)(h16)0;
-  }
-  half8_t ya[G::DS];
-  if (p.rope_mode == SC_ROPE_NONE) {
-    pack_unrotated<D>(x1, x2, ya);
-  } else {
-    const int pos = tv ? p.tail_pos[(long)b * p.TCAP + slot] : 0;
-    const int phi = clamp_angle(pos, p.rope_len);
-    rotate_pairs<D>(x1, x2, p.cos + phi * p.rope_stride, p.sin + phi * p.rope_stride, g,
-                    p.rope_mode == SC_ROPE_DISTANCE ? kRotDist : kRotTailAbs, p.halves_equal != 0, ya);
-  }
-  float4_t sacc = (float4_t)0.f;
-#pragma unroll
-  for (int s = 0; s < G::DS; ++s) sacc = mfma_16x16x32(ya[s], qb[s], sacc);
-
-  const long cache_off = (long)ncold * p.TB;  // tail follows the cold blocks
-  const uint8_t* mrow = (p.mask && hv) ? p.mask + b * p.mask_sb + (long)(h * nrep + n) * p.mask_sh + cache_off : nullptr;
-  float* lrow = (p.logits && hv) ? p.logits + b * p.lg_sb + (long)(h * nrep + n) * p.lg_sh + cache_off : nullptr;
-  float sc[4];
-  int vslot[4];
-#pragma unroll
-  for (int jj = 0; jj < 4; ++jj) {
-    const int tt = tile0 + 4 * g + jj;
-    const bool valid = tt < tl;
-    vslot[jj] = valid ? (th + tt) % p.TCAP : -1;
-    const float raw = sacc[jj];
-    if (lrow && valid) lrow[tt] = raw * p.scale;
-    bool k = hv && valid;
-    if (k && mrow) k = mrow[tt] != 0;
-    sc[jj] = k ? raw * p.scale_log2 : -INFINITY;
-  }
-  const float m_w = max_over_rows(fmaxf(fmaxf(sc[0], sc[1]), fmaxf(sc[2], sc[3])));
-  const bool live = m_w != -INFINITY;
-  float pv[4];
-#pragma unroll
-  for (int jj = 0; jj < 4; ++jj) pv[jj] = live ? exp2f(sc[jj] - m_w) : 0.f;
-  const float l_w = sum_over_rows(pv[0] + pv[1] + pv[2] + pv[3]);
-  const half4_t pb = {(h16)pv[0], (h16)pv[1], (h16)pv[2], (h16)pv[3]};
-
-  // O^T[d][head] = V^T[d][tok] . P[tok][head]
-  float4_t oacc[G::MT];
-  const h16* vbase = p.tail_v + bh * p.TCAP * D;
-#pragma unroll
-  for (int mt = 0; mt < G::MT; ++mt) {
-    h16 va[4];
-#pragma unroll
-    for (int jj = 0; jj < 4; ++jj) va[jj] = vslot[jj] >= 0 ? vbase[(long)vslot[jj] * D + mt * 16 + n] : (h16)0;
-    oacc[mt] = mfma_16x16x16((half4_t){va[0], va[1], va[2], va[3]}, pb, (float4_t)0.f);
-  }
-
-  float* s_m = lds;                    // [kWaves][nrep]
-  float* s_l = s_m + kWaves * nrep;    // [kWaves][nrep]
-  float* s_acc = s_l + kWaves * nrep;  // [kWaves][nrep][D]
-  if (hv) {
-    if (g == 0) {
-      s_m[w * nrep + n] = m_w;
-      s_l[w * nrep + n] = l_w;
+    for (int i = 0; i < kTailTiles; ++i) {
+      const long r = (long)clamp_angle(kpos[i], p.rope_len) * p.rope_stride + g * G::QG;
+      rc[i] = load_h8s<G::NV>(p.cos + r);
+      rs[i] = load_h8s<G::NV>(p.sin + r);
     }
-#pragma unroll
-    for (int mt = 0; mt < G::MT; ++mt)
-#pragma unroll
-      for (int jj = 0; jj < 4; ++jj) s_acc[(w * nrep + n) * D + mt * 16 + 4 * g + jj] = oacc[mt][jj];
   }
-  __syncthreads();
+  // stage V tiles in LDS ([tile][16 tokens][kVRow]); 8-byte stores
+  h16* vs = reinterpret_cast<h16*>(lds) + (long)w * kTailTiles * kTile * kVRow;
+#pragma unroll
+  for (int i = 0; i < kTailTiles; ++i)
+#pragma unroll
+    for (int q = 0; q < QPR; ++q) {
+      h16* dst = vs + (i * kTile + vr) * kVRow + vqtr * (D / 4) + 8 * q;
+      const half8_t v = vq[i][q];
+      *reinterpret_cast<half4_t*>(dst) = (half4_t){v[0], v[1], v[2], v[3]};
+      *reinterpret_cast<half4_t*>(dst + 4) = (half4_t){v[4], v[5], v[6], v[7]};
+    }
+
+  const long cache_off = (long)ncold * p.TB;  // tail follows the cold blocks in cache order
+  const uint8_t* mrow = nullptr;
+  float* lrow = nullptr;
+  if constexpr (GEN) {
+    mrow = (p.mask && hv) ? p.mask + b * p.mask_sb + (long)(h * nrep + n) * p.mask_sh + cache_off : nullptr;
+    lrow = (p.logits && hv) ? p.logits + b * p.lg_sb + (long)(h * nrep + n) * p.lg_sh + cache_off : nullptr;
+  }
+  // ---- A. scores
+  half4_t lg[kTailTiles];
+#pragma unroll
+  for (int i = 0; i < kTailTiles; ++i) {
+    const int tile0 = wtok0 + i * kTile;
+    half8_t ya[G::DS];
+    if constexpr (!GEN) {
+      rotate_he<D>(kx1[i], kx2[i], rc[i], rs[i], ya);
+    } else {
+      if (!rope) {
+        unrotated<D>(kx1[i], kx2[i], ya);
+      } else if (he) {
+        rotate_he<D>(kx1[i], kx2[i], rc[i], rs[i], ya);
+      } else {
+        const long r2 = (long)clamp_angle(kpos[i], p.rope_len) * p.rope_stride + g * G::QG + G::HALF;
+        const Half8s<G::NV> c2 = load_h8s<G::NV>(p.cos + r2), s2 = load_h8s<G::NV>(p.sin + r2);
+        rotate<D>(kx1[i], kx2[i], rc[i], rs[i], c2, s2, kind, ya);
+      }
+    }
+    float4_t sacc = (float4_t)0.f;
+#pragma unroll
+    for (int s = 0; s < G::DS; ++s) sacc = mfma_16x16x32(ya[s], qb[s], sacc);
+#pragma unroll
+    for (int jj = 0; jj < 4; ++jj) {
+      const int tt = tile0 + 4 * g + jj;
+      const bool valid = tt < tl;
+      h16 l16 = fp16_logit(sacc[jj], p.scale);
+      if constexpr (GEN) {
+        if (lrow && valid) lrow[tt] = (float)l16;
+        if (mrow && valid && mrow[tt] == 0) l16 = (h16)(-INFINITY);
+      }
+      lg[i][jj] = valid ? l16 : (h16)(-INFINITY);
+    }
+  }
+  __syncthreads();  // staged V tiles visible to the whole wave
+  // ---- B. maximum; C. probabilities and P . V
+  const float m2 = max_over_rows(lane_max_log2<kTailTiles>(lg));
+  const float msub = (m2 == -INFINITY) ? 0.f : m2;
+  float l_run = 0.f;
+  float4_t oacc[G::MT];
+#pragma unroll
+  for (int mt = 0; mt < G::MT; ++mt) oacc[mt] = (float4_t)0.f;
+#pragma unroll
+  for (int i = 0; i < kTailTiles; ++i) {
+    float pv[4];
+#pragma unroll
+    for (int jj = 0; jj < 4; ++jj) {
+      pv[jj] = fast_exp2(__builtin_fmaf((float)lg[i][jj], kLog2e, -msub));
+      l_run += pv[jj];
+    }
+    const half4_t pb = {(h16)pv[0], (h16)pv[1], (h16)pv[2], (h16)pv[3]};
+    // O^T[d][head] += V^T[d][tok] . P[tok][head]; V^T read from the staged tile
+    const h16* vt = vs + (i * kTile + 4 * g) * kVRow + n;
+#pragma unroll
+    for (int mt = 0; mt < G::MT; ++mt) {
+      const half4_t va = {vt[16 * mt], vt[kVRow + 16 * mt], vt[2 * kVRow + 16 * mt], vt[3 * kVRow + 16 * mt]};
+      oacc[mt] = mfma_16x16x16(va, pb, oacc[mt]);
+    }
+  }
+  l_run = sum_over_rows(l_run);
+  __syncthreads();  // the staged tiles are overwritten by the merge below
+  float accv[4 * G::MT];
+#pragma unroll
+  for (int mt = 0; mt < G::MT; ++mt)
+#pragma unroll
+    for (int jj = 0; jj < 4; ++jj) accv[4 * mt + jj] = oacc[mt][jj];
+  float *s_mrg, *s_ml;
+  merge_waves<D>(lds, nrep, w, g, n, hv, m2, l_run, accv, 1.0f, s_mrg, s_ml);
   for (int idx = threadIdx.x; idx < nrep * D; idx += kThreads) {
     const int hh = idx / D, d = idx % D;
-    float M = -INFINITY;
-#pragma unroll
-    for (int ww = 0; ww < kWaves; ++ww) M = fmaxf(M, s_m[ww * nrep + hh]);
-    float acc = 0.f, L = 0.f;
-    if (M != -INFINITY) {
-#pragma unroll
-      for (int ww = 0; ww < kWaves; ++ww) {
-        const float mw = s_m[ww * nrep + hh];
-        const float a = (mw == -INFINITY) ? 0.f : exp2f(mw - M);
-        acc += a * s_acc[(ww * nrep + hh) * D + d];
-        L += a * s_l[ww * nrep + hh];
-      }
-    }
-    float* r = record_ptr(p, b, h, unit, hh, G::PREC);
-    r[2 + d] = acc;
-    if (d == 0) {
-      r[0] = M;
-      r[1] = L;
-    }
+    record_ptr(p, b, h, unit, hh, G::PREC)[4 + d] = s_mrg[idx];
+  }
+  if ((int)threadIdx.x < nrep) {
+    float* r = record_ptr(p, b, h, unit, threadIdx.x, G::PREC);
+    r[0] = s_ml[2 * threadIdx.x];
+    r[1] = s_ml[2 * threadIdx.x + 1];
   }
 }
 
-template <int D, int KK, int KV>
-__global__ __launch_bounds__(kThreads) void decode_partial_kernel(DecodeParams p) {
-  extern __shared__ float lds[];
-  const int u = xcd_remap(blockIdx.x, p.total_units);
-  if (u >= p.total_units) return;
-  const int nbh = p.B * p.Hkv;
-  const int chunk = u / nbh, bh = u % nbh;
-  const int b = bh / p.Hkv, h = bh % p.Hkv;
-  if (chunk < p.grid_blocks)
-    cold_unit<D, KK, KV>(p, b, h, chunk, lds);
-  else
-    tail_unit<D>(p, b, h, chunk - p.grid_blocks, lds);
+// Workgroup x runs on XCD x % 8 (round-robin dispatch).  Each XCD gets an
+// equal share of the tail units (first) and a contiguous, equal share of
+// the cold units in chunk-major order, so concurrently running units of
+// one XCD read the same cos/sin rows from its L2.
+template <int D, int KK, int KV, int TPW, bool GEN>
+__global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(2))) void decode_partial_kernel(DecodeParams p) {
+  extern __shared__ __align__(16) char smem[];
+  const long xcd = blockIdx.x & 7, slot = blockIdx.x >> 3;
+  const long t_lo = xcd * p.n_tail_units / 8, t_hi = (xcd + 1) * p.n_tail_units / 8;
+  const long c_lo = xcd * p.n_cold_units / 8, c_hi = (xcd + 1) * p.n_cold_units / 8;
+  if (slot < t_hi - t_lo) {
+    const int nbh = p.B * p.Hkv;
+    const long u = t_lo + slot;
+    const int chunk = (int)(u / nbh), bh = (int)(u % nbh);
+    tail_unit<D, GEN>(p, bh / p.Hkv, bh % p.Hkv, chunk, reinterpret_cast<float*>(smem));
+    return;
+  }
+  const long s2 = slot - (t_hi - t_lo);
+  if (s2 >= c_hi - c_lo) return;
+  const int nbq = p.B * p.n_hq;
+  const long u = c_lo + s2;
+  const int j = (int)(u / nbq), bq = (int)(u % nbq);
+  if constexpr (GEN) {
+    if (p.rope_mode != SC_ROPE_NONE && !p.halves_equal) {
+      cold_unit<D, KK, KV, TPW, GEN, false>(p, bq / p.n_hq, bq % p.n_hq, j, smem);
+      return;
+    }
+  }
+  cold_unit<D, KK, KV, TPW, GEN, true>(p, bq / p.n_hq, bq % p.n_hq, j, smem);
 }
 
-// Log-sum-exp merge of the partial records of one (sequence, KV head).
+// Log-sum-exp merge of the partial records of one (sequence, query head):
+// wave w folds the records u = w (mod 16), then the waves merge in LDS.
 template <int D>
-__global__ __launch_bounds__(256) void decode_combine_kernel(DecodeParams p) {
+__global__ __launch_bounds__(64 * kCombineWaves) void decode_combine_kernel(DecodeParams p) {
   constexpr int PREC = Geo<D>::PREC;
-  const int bh = blockIdx.x;
-  const int b = bh / p.Hkv, h = bh % p.Hkv;
-  for (int idx = threadIdx.x; idx < p.nrep * D; idx += blockDim.x) {
-    const int hh = idx / D, d = idx % D;
-    float M = -INFINITY;
-    for (int u = 0; u < p.units_per_bh; ++u) M = fmaxf(M, record_ptr(p, b, h, u, hh, PREC)[0]);
-    float L = 0.f, O = 0.f;
-    if (M != -INFINITY) {
-      for (int u = 0; u < p.units_per_bh; ++u) {
-        const float* r = record_ptr(p, b, h, u, hh, PREC);
-        const float m = r[0];
-        if (m == -INFINITY) continue;
-        const float a = exp2f(m - M);
-        L += a * r[1];
-        O += a * r[2 + d];
-      }
+  constexpr int E = D / 64;  // d values per lane
+  constexpr int U = 8;       // records in flight per wave
+  __shared__ float s_m[kCombineWaves], s_l[kCombineWaves], s_o[kCombineWaves][D];
+  const int bq = blockIdx.x;
+  const int b = bq / p.Hq, qh = bq % p.Hq;
+  const int h = qh / p.nrep, hh = qh % p.nrep;
+  const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
+  float M = -INFINITY, L = 0.f, O[E];
+#pragma unroll
+  for (int e = 0; e < E; ++e) O[e] = 0.f;
+  for (int u0 = w; u0 < p.units_per_bh; u0 += U * kCombineWaves) {
+    float mr[U], lr[U], orr[U][E];
+#pragma unroll
+    for (int k = 0; k < U; ++k) {
+      const int u = u0 + k * kCombineWaves;
+      const float* r = record_ptr(p, b, h, u < p.units_per_bh ? u : 0, hh, PREC);
+      const bool ok = u < p.units_per_bh;
+      mr[k] = ok ? r[0] : -INFINITY;
+      lr[k] = ok ? r[1] : 0.f;
+#pragma unroll
+      for (int e = 0; e < E; ++e) orr[k][e] = ok ? r[4 + lane + 64 * e] : 0.f;
     }
-    p.out[b * p.out_sb + (long)(h * p.nrep + hh) * p.out_sh + d] = (h16)(O / L);
+#pragma unroll
+    for (int k = 0; k < U; ++k) {
+      if (mr[k] == -INFINITY) continue;
+      const float Mn = fmaxf(M, mr[k]);
+      const float a = (M == -INFINITY) ? 0.f : fast_exp2(M - Mn);
+      const float bb = fast_exp2(mr[k] - Mn);
+      L = L * a + lr[k] * bb;
+#pragma unroll
+      for (int e = 0; e < E; ++e) O[e] = O[e] * a + orr[k][e] * bb;
+      M = Mn;
+    }
+  }
+  if (lane == 0) {
+    s_m[w] = M;
+    s_l[w] = L;
+  }
+#pragma unroll
+  for (int e = 0; e < E; ++e) s_o[w][lane + 64 * e] = O[e];
+  __syncthreads();
+  for (int d = threadIdx.x; d < D; d += 64 * kCombineWaves) {
+    float Mt = -INFINITY;
+#pragma unroll
+    for (int ww = 0; ww < kCombineWaves; ++ww) Mt = fmaxf(Mt, s_m[ww]);
+    float Lt = 0.f, Ot = 0.f;
+#pragma unroll
+    for (int ww = 0; ww < kCombineWaves; ++ww) {
+      if (s_m[ww] == -INFINITY) continue;
+      const float a = fast_exp2(s_m[ww] - Mt);
+      Lt += a * s_l[ww];
+      Ot += a * s_o[ww][d];
+    }
+    p.out[b * p.out_sb + (long)qh * p.out_sh + d] = (h16)(Ot / Lt);
   }
 }
 
 bool padded_rank_ok(int kp) { return kp == 16 || kp == 32 || kp == 64; }
+
+// Tiles of 16 tokens per wave and range (64-token ranges).
+constexpr int kTilesPerWave = 4;
 
 int fill_params(const ScDecodeArgs* a, DecodeParams* p) {
   if (!a || !a->tier) return sc_fail(SC_ERR_INVALID, "sc_decode_attn: null arguments");
@@ -543,6 +1010,13 @@ int fill_params(const ScDecodeArgs* a, DecodeParams* p) {
     return sc_fail(SC_ERR_INVALID, "cos/sin must be 16-byte aligned with row stride multiple of 8");
   if (a->mask && ((a->mask_stride_h & 3) || (a->mask_stride_b & 3) || ((uintptr_t)a->mask & 3)))
     return sc_fail(SC_ERR_INVALID, "mask must be 4-byte aligned with strides multiple of 4");
+  if (a->grid_blocks > 0 && (((uintptr_t)t->codes_k & 15) || ((uintptr_t)t->codes_v & 15) ||
+                             ((uintptr_t)t->basis_k & 15) || ((uintptr_t)t->basis_v & 15) ||
+                             ((uintptr_t)t->scales_k & 3) || ((uintptr_t)t->scales_v & 3)))
+    return sc_fail(SC_ERR_INVALID, "cold-tier arrays must be 16-byte aligned");
+  if (a->grid_tail > 0 && (((uintptr_t)t->tail_k & 15) || ((uintptr_t)t->tail_v & 15)))
+    return sc_fail(SC_ERR_INVALID, "tail arrays must be 16-byte aligned");
+  const int tpw = kTilesPerWave;
   p->B = t->batch;
   p->Hq = a->q_heads;
   p->Hkv = t->kv_heads;
@@ -555,11 +1029,14 @@ int fill_params(const ScDecodeArgs* a, DecodeParams* p) {
   p->rope_len = a->rope_len;
   p->halves_equal = a->halves_equal;
   p->grid_blocks = a->grid_blocks;
+  p->tpw = tpw;
+  p->n_hq = (t->kv_heads + kWaves - 1) / kWaves;
+  p->cold_units = p->grid_blocks;
   p->tail_units = (a->grid_tail + kTailUnit - 1) / kTailUnit;
-  p->units_per_bh = p->grid_blocks + p->tail_units;
-  p->total_units = p->units_per_bh * p->B * p->Hkv;
+  p->units_per_bh = p->cold_units + p->tail_units;
+  p->n_cold_units = (long)p->grid_blocks * p->B * p->n_hq;
+  p->n_tail_units = (long)p->tail_units * p->B * p->Hkv;
   p->scale = a->scale;
-  p->scale_log2 = a->scale * 1.4426950408889634f;
   p->q = (const h16*)a->q;
   p->q_sb = a->q_stride_b;
   p->q_sh = a->q_stride_h;
@@ -593,39 +1070,58 @@ int fill_params(const ScDecodeArgs* a, DecodeParams* p) {
 }
 
 size_t workspace_bytes(const DecodeParams& p, int D) {
-  return (size_t)p.B * p.Hkv * p.units_per_bh * p.nrep * (D + 2) * sizeof(float);
+  return (size_t)p.B * p.Hkv * p.units_per_bh * p.nrep * (D + 4) * sizeof(float);
 }
 
-template <int D, int KK, int KV>
+template <int D, int KK, int KV, int TPW, bool GEN>
 int launch(DecodeParams& p, hipStream_t s) {
-  const int grid = xcd_grid(p.total_units);
-  const size_t cold_lds = (size_t)(2 * kWaves * p.nrep + kWaves * p.nrep * KV + p.nrep * KV + 2 * p.nrep) * 4;
-  const size_t tail_lds = (size_t)(2 * kWaves * p.nrep + kWaves * p.nrep * D) * 4;
-  const size_t lds = cold_lds > tail_lds ? cold_lds : tail_lds;
+  long slots = 0;
+  for (int x = 0; x < 8; ++x) {
+    const long nt = (x + 1) * p.n_tail_units / 8 - x * p.n_tail_units / 8;
+    const long nc = (x + 1) * p.n_cold_units / 8 - x * p.n_cold_units / 8;
+    if (nt + nc > slots) slots = nt + nc;
+  }
+  const long grid = 8 * slots;
+  size_t lds = 0;
+  if (p.cold_units > 0 && (GEN ? p.rope_mode != SC_ROPE_NONE : true)) {
+    const bool he = !GEN || p.halves_equal;
+    lds = (size_t)2 * kTile * TPW * (he ? RopeStage<D, true>::ROW : RopeStage<D, false>::ROW);
+  }
+  if (p.tail_units > 0) {
+    const size_t merge_tail = (size_t)(2 * kWaves * p.nrep + kWaves * p.nrep * D + p.nrep * D + 2 * p.nrep) * 4;
+    const size_t stage_tail = (size_t)kWaves * kTailTiles * kTile * kVRow * 2;
+    if (merge_tail > lds) lds = merge_tail;
+    if (stage_tail > lds) lds = stage_tail;
+  }
   if (grid > 0) {
-    hipLaunchKernelGGL((decode_partial_kernel<D, KK, KV>), dim3(grid), dim3(kThreads), lds, s, p);
+    hipLaunchKernelGGL((decode_partial_kernel<D, KK, KV, TPW, GEN>), dim3((unsigned)grid), dim3(kThreads), lds, s, p);
     int rc = sc_launch_status("decode_partial_kernel");
     if (rc) return rc;
   }
-  hipLaunchKernelGGL((decode_combine_kernel<D>), dim3(p.B * p.Hkv), dim3(256), 0, s, p);
+  hipLaunchKernelGGL((decode_combine_kernel<D>), dim3(p.B * p.Hq), dim3(64 * kCombineWaves), 0, s, p);
   return sc_launch_status("decode_combine_kernel");
 }
 
-template <int D, int KK>
+template <int D, int KK, int KV, bool GEN>
+int dispatch_tpw(DecodeParams& p, hipStream_t s) {
+  return launch<D, KK, KV, kTilesPerWave, GEN>(p, s);
+}
+
+template <int D, int KK, bool GEN>
 int dispatch_kv(DecodeParams& p, int kv, hipStream_t s) {
   switch (kv) {
-    case 16: return launch<D, KK, 16>(p, s);
-    case 32: return launch<D, KK, 32>(p, s);
-    default: return launch<D, KK, 64>(p, s);
+    case 16: return dispatch_tpw<D, KK, 16, GEN>(p, s);
+    case 32: return dispatch_tpw<D, KK, 32, GEN>(p, s);
+    default: return dispatch_tpw<D, KK, 64, GEN>(p, s);
   }
 }
 
-template <int D>
+template <int D, bool GEN>
 int dispatch_kk(DecodeParams& p, int kk, int kv, hipStream_t s) {
   switch (kk) {
-    case 16: return dispatch_kv<D, 16>(p, kv, s);
-    case 32: return dispatch_kv<D, 32>(p, kv, s);
-    default: return dispatch_kv<D, 64>(p, kv, s);
+    case 16: return dispatch_kv<D, 16, GEN>(p, kv, s);
+    case 32: return dispatch_kv<D, 32, GEN>(p, kv, s);
+    default: return dispatch_kv<D, 64, GEN>(p, kv, s);
   }
 }
 
@@ -652,6 +1148,8 @@ extern "C" int sc_decode_attn(const ScDecodeArgs* args, void* workspace, size_t 
   p.ws = (float*)workspace;
   hipStream_t s = (hipStream_t)stream;
   const int kk = args->tier->kp_keys, kv = args->tier->kp_values;
-  if (D == 128) return dispatch_kk<128>(p, kk, kv, s);
-  return dispatch_kk<64>(p, kk, kv, s);
+  const bool gen = args->mask || args->logits_out || args->rope_mode == SC_ROPE_NONE || !args->halves_equal;
+  if (D == 128)
+    return gen ? dispatch_kk<128, true>(p, kk, kv, s) : dispatch_kk<128, false>(p, kk, kv, s);
+  return gen ? dispatch_kk<64, true>(p, kk, kv, s) : dispatch_kk<64, false>(p, kk, kv, s);
 }

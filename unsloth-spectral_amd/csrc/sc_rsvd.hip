@@ -685,7 +685,7 @@ __global__ __launch_bounds__(kThreads) void rsvd_tier_kernel(RsvdParams p) {
   j.r = kind ? p.r_v : p.r;
   j.kp = kind ? T.kp_values : T.kp_keys;
   j.coeff_major = kind;
-  j.basis_dmajor = !kind;
+  j.basis_dmajor = 1;  // both bases d-major [cols][kp]
   j.codes = (kind ? T.codes_v : T.codes_k) + bhs * TB * j.kp;
   j.scales = (kind ? T.scales_v : T.scales_k) + (per_row ? bhs * TB : bhs);
   j.minmax = (kind ? T.minmax_v : T.minmax_k) ? (kind ? T.minmax_v : T.minmax_k) + bhs * 2 : nullptr;

@@ -91,10 +91,10 @@ __global__ __launch_bounds__(kThreads) void dequant_kernel(DequantParams p) {
   const int8_t* ck = T.codes_k + bhj * TB * T.kp_keys + (long)t * T.kp_keys;
   const int8_t* cv = T.codes_v + bhj * T.kp_values * TB + t;
   const h16* bk = (const h16*)T.basis_k + bhj * (long)D * T.kp_keys + (long)d * T.kp_keys;
-  const h16* bv = (const h16*)T.basis_v + bhj * (long)T.kp_values * D + d;
+  const h16* bv = (const h16*)T.basis_v + bhj * (long)D * T.kp_values + (long)d * T.kp_values;
   float ak = 0.f, av = 0.f;
   for (int i = 0; i < T.k_keys; ++i) ak += (float)(h16)((float)ck[i] * sk) * (float)bk[i];
-  for (int i = 0; i < T.k_values; ++i) av += (float)(h16)((float)cv[(long)i * TB] * sv) * (float)bv[(long)i * D];
+  for (int i = 0; i < T.k_values; ++i) av += (float)(h16)((float)cv[(long)i * TB] * sv) * (float)bv[i];
   p.k_out[idx] = (h16)ak;
   p.v_out[idx] = (h16)av;
 }

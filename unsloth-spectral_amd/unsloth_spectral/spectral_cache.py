@@ -139,7 +139,7 @@ class SpectralCache:
         self.minmax_v = torch.zeros(B, H, NB, 2, dtype=torch.float32, device=dev)
         self.vnorm = torch.ones(B, H, NB, dtype=torch.float32, device=dev)
         self.basis_k = torch.zeros(B, H, NB, D, self.kp_keys, dtype=torch.float16, device=dev)
-        self.basis_v = torch.zeros(B, H, NB, self.kp_values, D, dtype=torch.float16, device=dev)
+        self.basis_v = torch.zeros(B, H, NB, D, self.kp_values, dtype=torch.float16, device=dev)
         self.block_start = torch.zeros(B, NB, dtype=torch.int32, device=dev)
         self.tail_k = torch.zeros(B, H, C, D, dtype=torch.float16, device=dev)
         self.tail_v = torch.zeros(B, H, C, D, dtype=torch.float16, device=dev)
@@ -331,7 +331,7 @@ class SpectralCache:
             ck = self._dequant_coeffs(j, "K")
             cv = self._dequant_coeffs(j, "V")
             bk = self.basis_k[:, :, j, :, :self.k_rank_keys].transpose(-1, -2).contiguous()
-            bv = self.basis_v[:, :, j, :self.k_rank_values, :].contiguous()
+            bv = self.basis_v[:, :, j, :, :self.k_rank_values].transpose(-1, -2).contiguous()
             mk, mv = self.minmax_k[:, :, j], self.minmax_v[:, :, j]
             if squeeze:
                 ck, cv, bk, bv, mk, mv = ck[0], cv[0], bk[0], bv[0], mk[0], mv[0]
@@ -439,7 +439,7 @@ class SpectralCache:
             c.scales_k[:, :, :NB] = scales_k
             c.scales_v[:, :, :NB] = scales_v
             c.basis_k[:, :, :NB, :, :kK] = basis_k.transpose(-1, -2).to(torch.float16)
-            c.basis_v[:, :, :NB, :kV, :] = basis_v.to(torch.float16)
+            c.basis_v[:, :, :NB, :, :kV] = basis_v.transpose(-1, -2).to(torch.float16)
             c.block_start[:, :NB] = block_start.to(torch.int32)
             vmax = scales_v.reshape(B, H, NB, -1).amax(-1)
             _, e = torch.frexp(vmax)
