@@ -44,16 +44,14 @@ constexpr int kWaves = 4;
 constexpr int kThreads = 64 * kWaves;
 constexpr int kTile = 16;
 constexpr int kMaxRep = 16;
-constexpr int kTailTiles = 2;                           // tail tiles per wave
-constexpr int kTailUnit = kWaves * kTailTiles * kTile;  // tail tokens per unit
 constexpr int kVRow = 132;                              // LDS row (halves) of a staged V tile
 constexpr int kCombineWaves = 16;
 constexpr float kLog2e = 1.4426950408889634f;
 
 struct DecodeParams {
   int B, Hq, Hkv, nrep, TB, NB, TCAP, per_row, rope_mode, rope_len, halves_equal;
-  int grid_blocks, tpw, n_hq, cold_units, tail_units, units_per_bh;
-  long n_cold_units, n_tail_units;  // summed over (b, h)
+  int grid_blocks, tpw, n_hq, cold_units, units_per_bh, fold_tail;
+  long n_cold_units;  // summed over (b, head group)
   float scale;
   const h16* q;
   long q_sb, q_sh;
@@ -245,52 +243,6 @@ __device__ __forceinline__ float lane_max_log2(const half4_t (&lg)[NTILE]) {
   return fmaxf(a, c) * kLog2e;
 }
 
-// Merges the four waves' (m, l, acc[W]) in LDS.  Leaves the merged
-// accumulators in s_mrg[nrep][W] (scaled by post) and (M, L) in s_ml.
-template <int W>
-__device__ __forceinline__ void merge_waves(float* lds, int nrep, int w, int g, int n, bool hv, float m_run,
-                                            float l_run, const float* accv, float post, float*& s_mrg,
-                                            float*& s_ml) {
-  float* s_m = lds;                    // [kWaves][nrep]
-  float* s_l = s_m + kWaves * nrep;    // [kWaves][nrep]
-  float* s_acc = s_l + kWaves * nrep;  // [kWaves][nrep][W]
-  s_mrg = s_acc + kWaves * nrep * W;   // [nrep][W]
-  s_ml = s_mrg + nrep * W;             // [nrep][2]
-  if (hv) {
-    if (g == 0) {
-      s_m[w * nrep + n] = m_run;
-      s_l[w * nrep + n] = l_run;
-    }
-#pragma unroll
-    for (int t = 0; t < W / 16; ++t)
-#pragma unroll
-      for (int jj = 0; jj < 4; ++jj) s_acc[(w * nrep + n) * W + t * 16 + 4 * g + jj] = accv[4 * t + jj];
-  }
-  __syncthreads();
-  for (int idx = threadIdx.x; idx < nrep * W; idx += kThreads) {
-    const int hh = idx / W, i = idx % W;
-    float M = -INFINITY;
-#pragma unroll
-    for (int ww = 0; ww < kWaves; ++ww) M = fmaxf(M, s_m[ww * nrep + hh]);
-    float acc = 0.f, L = 0.f;
-    if (M != -INFINITY) {
-#pragma unroll
-      for (int ww = 0; ww < kWaves; ++ww) {
-        const float mw = s_m[ww * nrep + hh];
-        const float a = (mw == -INFINITY) ? 0.f : fast_exp2(mw - M);
-        acc += a * s_acc[(ww * nrep + hh) * W + i];
-        L += a * s_l[ww * nrep + hh];
-      }
-    }
-    s_mrg[idx] = acc * post;
-    if (i == 0) {
-      s_ml[2 * hh] = M;
-      s_ml[2 * hh + 1] = L;
-    }
-  }
-  __syncthreads();
-}
-
 // ------------------------------------------------------------------ cold
 // Staged RoPE rows.  LDS row rho of a range holds the cos/sin entries of
 // range token swap(rho) (bit fields [2:3] and [4:5] exchanged): the 16
@@ -394,14 +346,17 @@ __device__ __forceinline__ void load_vc(const DecodeParams& p, const CodeSrc<KK,
 }
 
 // Row scales of tokens 64 (i / 4) + 16 g + 4 (i % 4) + {0..3} of the range
-// (per row), or the block's scale four times (per head).
+// (per row), or the block's scale four times (per head).  PRM: 0 per head,
+// 1 per row, 2 decided at run time (general path).
+template <int PRM>
 __device__ __forceinline__ float4_t load_scale4(const DecodeParams& p, const float* base, int i) {
   const int g = (threadIdx.x & 63) >> 4;
-  if (p.per_row) return *reinterpret_cast<const float4_t*>(base + 64 * (i / 4) + 16 * g + 4 * (i % 4));
+  if (PRM == 1 || (PRM == 2 && p.per_row))
+    return *reinterpret_cast<const float4_t*>(base + 64 * (i / 4) + 16 * g + 4 * (i % 4));
   return (float4_t)base[0];
 }
 
-template <int KK, int KV, int TPW>
+template <int KK, int KV, int TPW, int PRM>
 __device__ __forceinline__ void load_codes(const DecodeParams& p, const CodeSrc<KK, KV, TPW>& s,
                                            CodeBuf<KK, KV, TPW>& cb) {
   using CB = CodeBuf<KK, KV, TPW>;
@@ -411,8 +366,8 @@ __device__ __forceinline__ void load_codes(const DecodeParams& p, const CodeSrc<
   for (int gr = 0; gr < CB::NGRP; ++gr) load_vc<KK, KV, TPW>(p, s, gr, cb);
 #pragma unroll
   for (int i = 0; i < TPW; ++i) {
-    cb.sk[i] = load_scale4(p, s.skp, i);
-    cb.sv[i] = load_scale4(p, s.svp, i);
+    cb.sk[i] = load_scale4<PRM>(p, s.skp, i);
+    cb.sv[i] = load_scale4<PRM>(p, s.svp, i);
   }
 }
 
@@ -424,14 +379,15 @@ struct ColdState {
 };
 
 // Scores (phase A), one maximum (B), probabilities and P . C_V (C) of one
-// range, merged into the running state.  The RoPE rows of the next range
-// (if any) are fetched into registers before phase A and written to the
-// other LDS buffer after it; every code register is refilled with the next
-// range's data (nsrc, if any) right after its last use, so the next range's
-// HBM loads are in flight during this one.
-template <int D, int KK, int KV, int TPW, bool GEN, bool HE>
+// range, merged into the running state.  If another range follows (MORE),
+// its RoPE rows are fetched into registers before phase A and written to
+// the other LDS buffer after it, and every code register is refilled with
+// its data (nsrc) right after its last use, so the next range's HBM loads
+// are in flight during this one.  MORE and PRM are compile-time so that the
+// tile loop has no branches and the compiler can overlap tiles.
+template <int D, int KK, int KV, int TPW, bool GEN, bool HE, int PRM, bool MORE>
 __device__ __forceinline__ void cold_range(const DecodeParams& p, CodeBuf<KK, KV, TPW>& cb,
-                                           const CodeSrc<KK, KV, TPW> nsrc, bool reload,
+                                           const CodeSrc<KK, KV, TPW> nsrc,
                                            const half8_t (&a8)[Geo<D>::MT][CodeBuf<KK, KV, TPW>::KC],
                                            const half4_t (&a4)[Geo<D>::MT], const half8_t (&qb)[Geo<D>::DS],
                                            const char* rope_cur, char* rope_next, int next_pos0, int qp, bool dist,
@@ -442,19 +398,19 @@ __device__ __forceinline__ void cold_range(const DecodeParams& p, CodeBuf<KK, KV
   using RS = RopeStage<D, HE>;
   constexpr int NSTG = (TPW * kTile) * RS::CH / kThreads;  // staged chunks per thread
   const int lane = threadIdx.x & 63, g = lane >> 4, n = lane & 15;
-  const bool stage = rope && rope_next != nullptr;
+  const bool stage = MORE && rope;
   // The next range's RoPE rows (L2 hits) are requested before any of this
   // range's HBM refills: vmcnt retires in order, so waiting for them before
   // the LDS stores below never waits for the refills.
-  // (Loaded whenever the tables exist: past the last range the angles are
-  // clamped into the table, and only the stores below are skipped.)
   uint4 sv[NSTG];
   int sd[NSTG];
+  if constexpr (MORE) {
 #pragma unroll
-  for (int k = 0; k < NSTG; ++k) {
-    const StageChunk<D, HE> sc = stage_chunk<D, HE>(p, k, next_pos0, qp, dist);
-    sv[k] = rope ? *sc.src : uint4{0, 0, 0, 0};
-    sd[k] = sc.dst;
+    for (int k = 0; k < NSTG; ++k) {
+      const StageChunk<D, HE> sc = stage_chunk<D, HE>(p, k, next_pos0, qp, dist);
+      sv[k] = rope ? *sc.src : uint4{0, 0, 0, 0};
+      sd[k] = sc.dst;
+    }
   }
   half4_t lg[TPW];
 #pragma unroll
@@ -463,14 +419,14 @@ __device__ __forceinline__ void cold_range(const DecodeParams& p, CodeBuf<KK, KV
     float4_t x[G::MT];
     if constexpr (KK == 16) {
       const half4_t bc = i8x4_to_h4(cb.kc[i][0]);
-      if (reload) load_kc<KK, KV, TPW>(nsrc, i, cb);
+      if constexpr (MORE) load_kc<KK, KV, TPW>(nsrc, i, cb);
 #pragma unroll
       for (int mt = 0; mt < G::MT; ++mt) x[mt] = mfma_16x16x16(a4[mt], bc, (float4_t)0.f);
     } else {
       half8_t bc[CB::KC];
 #pragma unroll
       for (int c = 0; c < CB::KC; ++c) bc[c] = i8x8_to_h8(cb.kc[i][c]);
-      if (reload) load_kc<KK, KV, TPW>(nsrc, i, cb);
+      if constexpr (MORE) load_kc<KK, KV, TPW>(nsrc, i, cb);
 #pragma unroll
       for (int mt = 0; mt < G::MT; ++mt) {
         float4_t acc = (float4_t)0.f;
@@ -506,7 +462,7 @@ __device__ __forceinline__ void cold_range(const DecodeParams& p, CodeBuf<KK, KV
     const int tg = gr * 64 + 16 * g + 4 * ii;
 #pragma unroll
     for (int jj = 0; jj < 4; ++jj) lg[i][jj] = fp16_logit(sacc[jj] * cb.sk[i][jj], p.scale);
-    if (reload) cb.sk[i] = load_scale4(p, nsrc.skp, i);
+    if constexpr (MORE) cb.sk[i] = load_scale4<PRM>(p, nsrc.skp, i);
     if constexpr (GEN) {
       uint32_t keep = 0xffffffffu;
       if (mrow) keep = *reinterpret_cast<const uint32_t*>(mrow + tg);
@@ -517,9 +473,11 @@ __device__ __forceinline__ void cold_range(const DecodeParams& p, CodeBuf<KK, KV
       }
     }
   }
-  if (stage) {
+  if constexpr (MORE) {
+    if (stage) {
 #pragma unroll
-    for (int k = 0; k < NSTG; ++k) *reinterpret_cast<uint4*>(rope_next + sd[k]) = sv[k];
+      for (int k = 0; k < NSTG; ++k) *reinterpret_cast<uint4*>(rope_next + sd[k]) = sv[k];
+    }
   }
   // ---- B. range maximum, merged into the running maximum
   const float mr = max_over_rows(lane_max_log2<TPW>(lg));
@@ -542,24 +500,169 @@ __device__ __forceinline__ void cold_range(const DecodeParams& p, CodeBuf<KK, KV
     }
     const float4_t svn = cb.sv[i] * vn;
     const half4_t pb = {(h16)(pv[0] * svn[0]), (h16)(pv[1] * svn[1]), (h16)(pv[2] * svn[2]), (h16)(pv[3] * svn[3])};
-    if (reload) cb.sv[i] = load_scale4(p, nsrc.svp, i);
+    if constexpr (MORE) cb.sv[i] = load_scale4<PRM>(p, nsrc.svp, i);
 #pragma unroll
     for (int nt = 0; nt < CB::NT; ++nt) {
       const uint4 w4 = cb.vc[gr][nt];
       const uint32_t word = ii == 0 ? w4.x : ii == 1 ? w4.y : ii == 2 ? w4.z : w4.w;
       st.pacc[nt] = mfma_16x16x16(i8x4_to_h4(word), pb, st.pacc[nt]);
     }
-    if (ii == 3 && reload) load_vc<KK, KV, TPW>(p, nsrc, gr, cb);
+    if constexpr (MORE) {
+      if (ii == 3) load_vc<KK, KV, TPW>(p, nsrc, gr, cb);
+    }
   }
 }
 
-// Cold unit: one workgroup per (sequence b, cold block j, group of four KV
-// heads); wave w is KV head 4 hq + w.  The block is walked in ranges of
+// Softmax state carried through the tail tiles: running max (log2 domain),
+// lane-partial sum and the accumulated rescale of the cold accumulators.
+struct TailState {
+  float m2, l, scale;
+};
+
+// Loads of one FP16 tail tile (16 tokens of one KV head): the key row of
+// token t0 + n (RoPE pairs of lane group g), its position, and the quarter
+// V row of token t0 + lane / 4 that the lane stages.
+template <int D>
+struct TailFetch {
+  Half8s<Geo<D>::NV> kx1, kx2;
+  half8_t vq[D / 32];
+  int kpos;
+};
+
+template <int D>
+__device__ __forceinline__ void tail_fetch(const DecodeParams& p, int b, int h, int t0, int tl, int th,
+                                           TailFetch<D>& f) {
+  using G = Geo<D>;
+  const int lane = threadIdx.x & 63, g = lane >> 4, n = lane & 15;
+  const long bh = (long)(b * p.Hkv + h);
+  const int t = t0 + n;
+  const int slot = (th + (t < tl ? t : 0)) % p.TCAP;
+  f.kpos = p.tail_pos[(long)b * p.TCAP + slot];
+  const h16* krow = p.tail_k + (bh * p.TCAP + slot) * D + g * G::QG;
+  f.kx1 = load_h8s<G::NV>(krow);
+  f.kx2 = load_h8s<G::NV>(krow + G::HALF);
+  const int t2 = t0 + (lane >> 2);
+  const int vslot = (th + (t2 < tl ? t2 : 0)) % p.TCAP;
+  const h16* vrow = p.tail_v + (bh * p.TCAP + vslot) * D + (lane & 3) * (D / 4);
+#pragma unroll
+  for (int q = 0; q < D / 32; ++q) f.vq[q] = *reinterpret_cast<const half8_t*>(vrow + 8 * q);
+}
+
+// One FP16 tail tile (tokens t0 .. t0 + 15 of one KV head, loads in f),
+// merged into the wave's running softmax state.  Scores use the fp16
+// pre-RoPE keys rotated at their stored positions; P.V accumulates in oacc
+// (O^T layout: lane (g, n) holds O[head n][16 mt + 4 g + jj]).  The V tile is
+// transposed through a wave-private LDS region.
+template <int D, bool GEN, bool HE>
+__device__ __forceinline__ void tail_tile(const DecodeParams& p, int b, int h, int t0, int tl, int ncold,
+                                          const half8_t (&qb)[Geo<D>::DS], h16* vs, TailFetch<D> f, TailState& sm,
+                                          float4_t (&oacc)[Geo<D>::MT]) {
+  using G = Geo<D>;
+  constexpr int QPR = D / 32;  // 16-byte chunks per quarter of a V row
+  const int lane = threadIdx.x & 63, g = lane >> 4, n = lane & 15;
+  const int vr = lane >> 2, vqtr = lane & 3;
+  const bool hv = n < p.nrep;
+  const bool rope = !GEN || p.rope_mode != SC_ROPE_NONE;
+  if (t0 + n >= tl) {
+#pragma unroll
+    for (int v = 0; v < G::NV; ++v) f.kx1.v[v] = f.kx2.v[v] = (half8_t)(h16)0;
+  }
+  if (t0 + vr >= tl) {
+#pragma unroll
+    for (int q = 0; q < QPR; ++q) f.vq[q] = (half8_t)(h16)0;
+  }
+  half8_t ya[G::DS];
+  if (!rope) {
+    unrotated<D>(f.kx1, f.kx2, ya);
+  } else {
+    const long r = (long)clamp_angle(f.kpos, p.rope_len) * p.rope_stride + g * G::QG;
+    const Half8s<G::NV> c1 = load_h8s<G::NV>(p.cos + r), s1 = load_h8s<G::NV>(p.sin + r);
+    if constexpr (HE) {
+      rotate_he<D>(f.kx1, f.kx2, c1, s1, ya);
+    } else {
+      const Half8s<G::NV> c2 = load_h8s<G::NV>(p.cos + r + G::HALF), s2 = load_h8s<G::NV>(p.sin + r + G::HALF);
+      rotate<D>(f.kx1, f.kx2, c1, s1, c2, s2, p.rope_mode == SC_ROPE_DISTANCE ? kRotDist : kRotTailAbs, ya);
+    }
+  }
+  // stage the V tile ([16 tokens][kVRow]); 8-byte stores, wave-private
+#pragma unroll
+  for (int q = 0; q < QPR; ++q) {
+    h16* dst = vs + vr * kVRow + vqtr * (D / 4) + 8 * q;
+    const half8_t v = f.vq[q];
+    *reinterpret_cast<half4_t*>(dst) = (half4_t){v[0], v[1], v[2], v[3]};
+    *reinterpret_cast<half4_t*>(dst + 4) = (half4_t){v[4], v[5], v[6], v[7]};
+  }
+  float4_t sacc = (float4_t)0.f;
+#pragma unroll
+  for (int s = 0; s < G::DS; ++s) sacc = mfma_16x16x32(ya[s], qb[s], sacc);
+  const long cache_off = (long)ncold * p.TB;  // tail follows the cold blocks in cache order
+  half4_t lg1[1];
+#pragma unroll
+  for (int jj = 0; jj < 4; ++jj) {
+    const int tk = t0 + 4 * g + jj;
+    const bool valid = tk < tl;
+    h16 l16 = fp16_logit(sacc[jj], p.scale);
+    if constexpr (GEN) {
+      if (p.logits && hv && valid) p.logits[b * p.lg_sb + (long)(h * p.nrep + n) * p.lg_sh + cache_off + tk] = (float)l16;
+      if (p.mask && hv && valid && p.mask[b * p.mask_sb + (long)(h * p.nrep + n) * p.mask_sh + cache_off + tk] == 0)
+        l16 = (h16)(-INFINITY);
+    }
+    lg1[0][jj] = valid ? l16 : (h16)(-INFINITY);
+  }
+  const float mt = max_over_rows(lane_max_log2<1>(lg1));
+  const float m_new = fmaxf(sm.m2, mt);
+  const float msub = (m_new == -INFINITY) ? 0.f : m_new;
+  const float alpha = fast_exp2(sm.m2 - msub);
+  sm.m2 = m_new;
+  sm.l *= alpha;
+  sm.scale *= alpha;  // rescale of the cold accumulators (applied by the caller)
+  float pv[4];
+#pragma unroll
+  for (int jj = 0; jj < 4; ++jj) {
+    pv[jj] = fast_exp2(__builtin_fmaf((float)lg1[0][jj], kLog2e, -msub));
+    sm.l += pv[jj];
+  }
+  const half4_t pb = {(h16)pv[0], (h16)pv[1], (h16)pv[2], (h16)pv[3]};
+  __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+  __builtin_amdgcn_wave_barrier();
+  __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+  const h16* vt = vs + 4 * g * kVRow + n;
+#pragma unroll
+  for (int m = 0; m < G::MT; ++m) {
+    const half4_t va = {vt[16 * m], vt[kVRow + 16 * m], vt[2 * kVRow + 16 * m], vt[3 * kVRow + 16 * m]};
+    oacc[m] = mfma_16x16x16(va, pb, oacc[m] * alpha);
+  }
+  __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+  __builtin_amdgcn_wave_barrier();
+  __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+}
+
+// Tail tiles j, j + W, ... (W workgroups per sequence and head group) for a
+// workgroup's wave; `first` holds the already issued loads of tile j.
+template <int D, bool GEN, bool HE>
+__device__ __forceinline__ void tail_tiles(const DecodeParams& p, int b, int h, int j, const half8_t (&qb)[Geo<D>::DS],
+                                           char* vstage, const TailFetch<D>& first, TailState& sm,
+                                           float4_t (&oacc)[Geo<D>::MT]) {
+  const int* cnt = p.counters + b * SC_NCOUNTERS;
+  const int tl = cnt[SC_CNT_TAIL_LEN], th = cnt[SC_CNT_TAIL_HEAD], ncold = cnt[SC_CNT_NCOLD];
+  const int ntile = (tl + kTile - 1) / kTile;
+  h16* vs = reinterpret_cast<h16*>(vstage);
+  tail_tile<D, GEN, HE>(p, b, h, j * kTile, tl, ncold, qb, vs, first, sm, oacc);
+  for (int tt = j + p.units_per_bh; tt < ntile; tt += p.units_per_bh) {
+    TailFetch<D> f;
+    tail_fetch<D>(p, b, h, tt * kTile, tl, th, f);
+    tail_tile<D, GEN, HE>(p, b, h, tt * kTile, tl, ncold, qb, vs, f, sm, oacc);
+  }
+}
+
+// Unit j of (sequence b, group of four KV heads hq): wave w is KV head
+// 4 hq + w.  Cold block j (if the sequence has it) is walked in ranges of
 // T = 16 TPW tokens; the RoPE rows of a range are staged once per
 // workgroup in LDS (double-buffered) and the INT8 codes of the next range
 // are in flight (ping-pong register buffers) while the current one is
-// processed.  Each wave writes one partial record per block.
-template <int D, int KK, int KV, int TPW, bool GEN, bool HE>
+// processed.  Then tail tile j (16 FP16 tokens, if present) is folded in.
+// Each wave writes one partial record per unit.
+template <int D, int KK, int KV, int TPW, bool GEN, bool HE, int PRM>
 __device__ void cold_unit(const DecodeParams& p, int b, int hq, int j, char* smem) {
   using G = Geo<D>;
   using CB = CodeBuf<KK, KV, TPW>;
@@ -571,11 +674,41 @@ __device__ void cold_unit(const DecodeParams& p, int b, int hq, int j, char* sme
   const int h = hq * kWaves + w;
   const bool hvalid = h < p.Hkv;
   const int ncold = p.counters[b * SC_NCOUNTERS + SC_CNT_NCOLD];
-  if (j >= ncold) {  // uniform over the workgroup
-    if (hvalid && lane < p.nrep) {
-      float* r = record_ptr(p, b, h, j, lane, G::PREC);
-      r[0] = -INFINITY;
-      r[1] = 0.f;
+  if (j >= ncold) {  // uniform over the workgroup: no cold block, tail tiles only
+    if (!hvalid) return;
+    const bool hv0 = n < p.nrep;
+    half8_t qt[G::DS];
+    if (hv0) {
+      load_q<D>(p, b, h, g, n, true, qt);
+    } else {
+#pragma unroll
+      for (int s = 0; s < G::DS; ++s) qt[s] = (half8_t)(h16)0;
+    }
+    TailState sm;
+    sm.m2 = -INFINITY;
+    sm.l = 0.f;
+    sm.scale = 0.f;
+    float4_t oacc[G::MT];
+#pragma unroll
+    for (int m = 0; m < G::MT; ++m) oacc[m] = (float4_t)0.f;
+    const bool he = !GEN || p.halves_equal != 0;
+    const int* cnt = p.counters + b * SC_NCOUNTERS;
+    if (p.fold_tail && j * kTile < cnt[SC_CNT_TAIL_LEN]) {
+      TailFetch<D> tf;
+      tail_fetch<D>(p, b, h, j * kTile, cnt[SC_CNT_TAIL_LEN], cnt[SC_CNT_TAIL_HEAD], tf);
+      if (he)
+        tail_tiles<D, GEN, true>(p, b, h, j, qt, smem + w * kTile * kVRow * 2, tf, sm, oacc);
+      else if constexpr (GEN)
+        tail_tiles<D, GEN, false>(p, b, h, j, qt, smem + w * kTile * kVRow * 2, tf, sm, oacc);
+    }
+    sm.l = sum_over_rows(sm.l);
+    float* rec = record_ptr(p, b, h, j, hv0 ? n : 0, G::PREC);
+#pragma unroll
+    for (int m = 0; m < G::MT; ++m)
+      if (hv0) *reinterpret_cast<float4_t*>(rec + 4 + 16 * m + 4 * g) = oacc[m];
+    if (hv0 && g == 0) {
+      rec[0] = sm.m2;
+      rec[1] = sm.l;
     }
     return;
   }
@@ -603,17 +736,13 @@ __device__ void cold_unit(const DecodeParams& p, int b, int hq, int j, char* sme
 #pragma unroll
     for (int k = 0; k < NSTG; ++k) *reinterpret_cast<uint4*>(smem + dst[k]) = v[k];
   }
-  // Codes of DEPTH consecutive ranges are in flight: two for ranks up to
-  // 32, one for larger ranks (register budget).
-  constexpr int DEPTH = 1;
-  CB cb0, cb1;
+  CB cb0;  // codes of the current range, refilled in place with the next
   half8_t a8[G::MT][KC];
   half4_t a4[G::MT];
   half8_t qb[G::DS];
   float vn = 1.f;
   if (hvalid) {
-    load_codes<KK, KV, TPW>(p, code_src<KK, KV, TPW>(p, bhj, 0), cb0);
-    if (DEPTH == 2 && R > 1) load_codes<KK, KV, TPW>(p, code_src<KK, KV, TPW>(p, bhj, T), cb1);
+    load_codes<KK, KV, TPW, PRM>(p, code_src<KK, KV, TPW>(p, bhj, 0), cb0);
     // K basis as the A operand: row n of tile mt is d = perm(mt, n).
     const h16* bk = p.basis_k + bhj * (long)D * KK;
 #pragma unroll
@@ -649,17 +778,16 @@ __device__ void cold_unit(const DecodeParams& p, int b, int hq, int j, char* sme
   for (int nt = 0; nt < NT; ++nt) st.pacc[nt] = (float4_t)0.f;
   __syncthreads();
 
-  // ---- ranges: range rr uses cb0 / cb1 by parity (DEPTH 2) or cb0, and
-  // refills it with range rr + DEPTH right after each register's last use.
-  auto range = [&](int rr, CB& cb) {
-    const bool more = rr + 1 < R;
+  // ---- ranges (the last one peeled: no refill, no staging)
+  auto range = [&](auto more_tag, int rr) {
+    constexpr bool M = decltype(more_tag)::value;
     char* cur = smem + (rr & 1) * RBUF;
-    char* next = more ? smem + ((rr + 1) & 1) * RBUF : nullptr;
+    char* next = smem + ((rr + 1) & 1) * RBUF;
     if (hvalid) {
-      cold_range<D, KK, KV, TPW, GEN, HE>(p, cb, code_src<KK, KV, TPW>(p, bhj, (rr + DEPTH) * T), rr + DEPTH < R, a8, a4,
-                                          qb, cur, next, start + (rr + 1) * T, qp, dist, rope, vn,
-                                          mrow ? mrow + rr * T : nullptr, lrow ? lrow + rr * T : nullptr, st);
-    } else if (rope && more) {
+      cold_range<D, KK, KV, TPW, GEN, HE, PRM, M>(p, cb0, code_src<KK, KV, TPW>(p, bhj, (rr + 1) * T), a8, a4, qb,
+                                                   cur, next, start + (rr + 1) * T, qp, dist, rope, vn,
+                                                   mrow ? mrow + rr * T : nullptr, lrow ? lrow + rr * T : nullptr, st);
+    } else if (M && rope) {
       // idle head slot: still stage its share of the next range's rows
       uint4 v[NSTG];
       int dst[NSTG];
@@ -674,15 +802,29 @@ __device__ void cold_unit(const DecodeParams& p, int b, int hq, int j, char* sme
     }
     __syncthreads();
   };
-  if constexpr (DEPTH == 2) {
-    for (int rr = 0; rr < R; rr += 2) {
-      range(rr, cb0);
-      if (rr + 1 < R) range(rr + 1, cb1);
-    }
-  } else {
-    for (int rr = 0; rr < R; ++rr) range(rr, cb0);
-  }
+  for (int rr = 0; rr + 1 < R; ++rr) range(std::integral_constant<bool, true>(), rr);
+  // the first FP16 tail tile of this workgroup is loaded during the last range
+  TailFetch<D> tf;
+  const int tl = p.counters[b * SC_NCOUNTERS + SC_CNT_TAIL_LEN];
+  const bool has_tail = p.fold_tail && hvalid && j * kTile < tl;
+  if (has_tail) tail_fetch<D>(p, b, h, j * kTile, tl, p.counters[b * SC_NCOUNTERS + SC_CNT_TAIL_HEAD], tf);
+  range(std::integral_constant<bool, false>(), R - 1);
   if (!hvalid) return;
+  // ---- FP16 tail tiles of this workgroup, merged into the running state
+  float4_t oacc[G::MT];
+#pragma unroll
+  for (int m = 0; m < G::MT; ++m) oacc[m] = (float4_t)0.f;
+  if (has_tail) {
+    TailState sm;
+    sm.m2 = st.m2;
+    sm.l = st.l;
+    sm.scale = 1.f;  // collects the rescale of the cold accumulators
+    tail_tiles<D, GEN, HE>(p, b, h, j, qb, smem + w * kTile * kVRow * 2, tf, sm, oacc);
+    st.m2 = sm.m2;
+    st.l = sm.l;
+#pragma unroll
+    for (int nt = 0; nt < NT; ++nt) st.pacc[nt] *= sm.scale;
+  }
   st.l = sum_over_rows(st.l);
 
   // ---- projection O^T[d][head] = B_V^T[d][i] . Pacc[i][head] on MFMA; Pacc
@@ -714,7 +856,7 @@ __device__ void cold_unit(const DecodeParams& p, int b, int hq, int j, char* sme
       o = mfma_16x16x16(bvf[mt][nt], ph[nt], o);
       o = mfma_16x16x16(bvf[mt][nt], pl[nt], o);
     }
-    if (hv) *reinterpret_cast<float4_t*>(rec + 4 + 16 * mt + 4 * g) = o * ivn;
+    if (hv) *reinterpret_cast<float4_t*>(rec + 4 + 16 * mt + 4 * g) = o * ivn + oacc[mt];
   }
   if (hv && g == 0) {
     rec[0] = st.m2;
@@ -722,193 +864,30 @@ __device__ void cold_unit(const DecodeParams& p, int b, int hq, int j, char* sme
   }
 }
 
-// ------------------------------------------------------------------ tail
-template <int D, bool GEN>
-__device__ void tail_unit(const DecodeParams& p, int b, int h, int c, float* lds) {
-  using G = Geo<D>;
-  constexpr int QPR = D / 32;  // 16-byte chunks per quarter of a staged V row
-  const int lane = threadIdx.x & 63, w = threadIdx.x >> 6, g = lane >> 4, n = lane & 15;
-  const int unit = p.cold_units + c;
-  const int* cnt = p.counters + b * SC_NCOUNTERS;
-  const int tl = cnt[SC_CNT_TAIL_LEN], th = cnt[SC_CNT_TAIL_HEAD], ncold = cnt[SC_CNT_NCOLD];
-  if (c * kTailUnit >= tl) {  // uniform over the workgroup
-    write_empty(p, b, h, unit, G::PREC);
-    return;
-  }
-  const int nrep = p.nrep;
-  const bool hv = n < nrep;
-  const long bh = (long)(b * p.Hkv + h);
-  const int wtok0 = c * kTailUnit + w * (kTailTiles * kTile);  // first tail token of the wave
-
-  // ---- issue loads: key rows (lane n = token), positions, V quarter rows
-  Half8s<G::NV> kx1[kTailTiles], kx2[kTailTiles];
-  int kpos[kTailTiles];
-  half8_t vq[kTailTiles][QPR];
-  const int vr = lane >> 2, vqtr = lane & 3;
-#pragma unroll
-  for (int i = 0; i < kTailTiles; ++i) {
-    const int t = wtok0 + i * kTile + n;
-    const bool tv = t < tl;
-    const int slot = (th + (tv ? t : 0)) % p.TCAP;
-    const h16* krow = p.tail_k + (bh * p.TCAP + slot) * D + g * G::QG;
-    kx1[i] = load_h8s<G::NV>(krow);
-    kx2[i] = load_h8s<G::NV>(krow + G::HALF);
-    kpos[i] = p.tail_pos[(long)b * p.TCAP + slot];
-    if (!tv) {
-#pragma unroll
-      for (int v = 0; v < G::NV; ++v) kx1[i].v[v] = kx2[i].v[v] = (half8_t)(h16)0;
-    }
-    const int t2 = wtok0 + i * kTile + vr;
-    const bool vv = t2 < tl;
-    const int vslot = (th + (vv ? t2 : 0)) % p.TCAP;
-    const h16* vrow = p.tail_v + (bh * p.TCAP + vslot) * D + vqtr * (D / 4);
-#pragma unroll
-    for (int q = 0; q < QPR; ++q) {
-      const half8_t v = *reinterpret_cast<const half8_t*>(vrow + 8 * q);
-      vq[i][q] = vv ? v : (half8_t)(h16)0;
-    }
-  }
-  half8_t qb[G::DS];
-  load_q<D>(p, b, h, g, n, hv, qb);
-  const bool rope = !GEN || p.rope_mode != SC_ROPE_NONE;
-  const bool he = !GEN || p.halves_equal != 0;
-  const int kind = p.rope_mode == SC_ROPE_DISTANCE ? kRotDist : kRotTailAbs;
-  Half8s<G::NV> rc[kTailTiles], rs[kTailTiles];
-  if (rope) {
-#pragma unroll
-    for (int i = 0; i < kTailTiles; ++i) {
-      const long r = (long)clamp_angle(kpos[i], p.rope_len) * p.rope_stride + g * G::QG;
-      rc[i] = load_h8s<G::NV>(p.cos + r);
-      rs[i] = load_h8s<G::NV>(p.sin + r);
-    }
-  }
-  // stage V tiles in LDS ([tile][16 tokens][kVRow]); 8-byte stores
-  h16* vs = reinterpret_cast<h16*>(lds) + (long)w * kTailTiles * kTile * kVRow;
-#pragma unroll
-  for (int i = 0; i < kTailTiles; ++i)
-#pragma unroll
-    for (int q = 0; q < QPR; ++q) {
-      h16* dst = vs + (i * kTile + vr) * kVRow + vqtr * (D / 4) + 8 * q;
-      const half8_t v = vq[i][q];
-      *reinterpret_cast<half4_t*>(dst) = (half4_t){v[0], v[1], v[2], v[3]};
-      *reinterpret_cast<half4_t*>(dst + 4) = (half4_t){v[4], v[5], v[6], v[7]};
-    }
-
-  const long cache_off = (long)ncold * p.TB;  // tail follows the cold blocks in cache order
-  const uint8_t* mrow = nullptr;
-  float* lrow = nullptr;
-  if constexpr (GEN) {
-    mrow = (p.mask && hv) ? p.mask + b * p.mask_sb + (long)(h * nrep + n) * p.mask_sh + cache_off : nullptr;
-    lrow = (p.logits && hv) ? p.logits + b * p.lg_sb + (long)(h * nrep + n) * p.lg_sh + cache_off : nullptr;
-  }
-  // ---- A. scores
-  half4_t lg[kTailTiles];
-#pragma unroll
-  for (int i = 0; i < kTailTiles; ++i) {
-    const int tile0 = wtok0 + i * kTile;
-    half8_t ya[G::DS];
-    if constexpr (!GEN) {
-      rotate_he<D>(kx1[i], kx2[i], rc[i], rs[i], ya);
-    } else {
-      if (!rope) {
-        unrotated<D>(kx1[i], kx2[i], ya);
-      } else if (he) {
-        rotate_he<D>(kx1[i], kx2[i], rc[i], rs[i], ya);
-      } else {
-        const long r2 = (long)clamp_angle(kpos[i], p.rope_len) * p.rope_stride + g * G::QG + G::HALF;
-        const Half8s<G::NV> c2 = load_h8s<G::NV>(p.cos + r2), s2 = load_h8s<G::NV>(p.sin + r2);
-        rotate<D>(kx1[i], kx2[i], rc[i], rs[i], c2, s2, kind, ya);
-      }
-    }
-    float4_t sacc = (float4_t)0.f;
-#pragma unroll
-    for (int s = 0; s < G::DS; ++s) sacc = mfma_16x16x32(ya[s], qb[s], sacc);
-#pragma unroll
-    for (int jj = 0; jj < 4; ++jj) {
-      const int tt = tile0 + 4 * g + jj;
-      const bool valid = tt < tl;
-      h16 l16 = fp16_logit(sacc[jj], p.scale);
-      if constexpr (GEN) {
-        if (lrow && valid) lrow[tt] = (float)l16;
-        if (mrow && valid && mrow[tt] == 0) l16 = (h16)(-INFINITY);
-      }
-      lg[i][jj] = valid ? l16 : (h16)(-INFINITY);
-    }
-  }
-  __syncthreads();  // staged V tiles visible to the whole wave
-  // ---- B. maximum; C. probabilities and P . V
-  const float m2 = max_over_rows(lane_max_log2<kTailTiles>(lg));
-  const float msub = (m2 == -INFINITY) ? 0.f : m2;
-  float l_run = 0.f;
-  float4_t oacc[G::MT];
-#pragma unroll
-  for (int mt = 0; mt < G::MT; ++mt) oacc[mt] = (float4_t)0.f;
-#pragma unroll
-  for (int i = 0; i < kTailTiles; ++i) {
-    float pv[4];
-#pragma unroll
-    for (int jj = 0; jj < 4; ++jj) {
-      pv[jj] = fast_exp2(__builtin_fmaf((float)lg[i][jj], kLog2e, -msub));
-      l_run += pv[jj];
-    }
-    const half4_t pb = {(h16)pv[0], (h16)pv[1], (h16)pv[2], (h16)pv[3]};
-    // O^T[d][head] += V^T[d][tok] . P[tok][head]; V^T read from the staged tile
-    const h16* vt = vs + (i * kTile + 4 * g) * kVRow + n;
-#pragma unroll
-    for (int mt = 0; mt < G::MT; ++mt) {
-      const half4_t va = {vt[16 * mt], vt[kVRow + 16 * mt], vt[2 * kVRow + 16 * mt], vt[3 * kVRow + 16 * mt]};
-      oacc[mt] = mfma_16x16x16(va, pb, oacc[mt]);
-    }
-  }
-  l_run = sum_over_rows(l_run);
-  __syncthreads();  // the staged tiles are overwritten by the merge below
-  float accv[4 * G::MT];
-#pragma unroll
-  for (int mt = 0; mt < G::MT; ++mt)
-#pragma unroll
-    for (int jj = 0; jj < 4; ++jj) accv[4 * mt + jj] = oacc[mt][jj];
-  float *s_mrg, *s_ml;
-  merge_waves<D>(lds, nrep, w, g, n, hv, m2, l_run, accv, 1.0f, s_mrg, s_ml);
-  for (int idx = threadIdx.x; idx < nrep * D; idx += kThreads) {
-    const int hh = idx / D, d = idx % D;
-    record_ptr(p, b, h, unit, hh, G::PREC)[4 + d] = s_mrg[idx];
-  }
-  if ((int)threadIdx.x < nrep) {
-    float* r = record_ptr(p, b, h, unit, threadIdx.x, G::PREC);
-    r[0] = s_ml[2 * threadIdx.x];
-    r[1] = s_ml[2 * threadIdx.x + 1];
-  }
-}
-
-// Workgroup x runs on XCD x % 8 (round-robin dispatch).  Each XCD gets an
-// equal share of the tail units (first) and a contiguous, equal share of
-// the cold units in chunk-major order, so concurrently running units of
-// one XCD read the same cos/sin rows from its L2.
+// Workgroup x runs on XCD x % 8 (round-robin dispatch).  Each XCD gets a
+// contiguous, equal share of the units in chunk-major order, so
+// concurrently running units of one XCD read the same cos/sin rows from
+// its L2.
 template <int D, int KK, int KV, int TPW, bool GEN>
 __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(2))) void decode_partial_kernel(DecodeParams p) {
   extern __shared__ __align__(16) char smem[];
   const long xcd = blockIdx.x & 7, slot = blockIdx.x >> 3;
-  const long t_lo = xcd * p.n_tail_units / 8, t_hi = (xcd + 1) * p.n_tail_units / 8;
   const long c_lo = xcd * p.n_cold_units / 8, c_hi = (xcd + 1) * p.n_cold_units / 8;
-  if (slot < t_hi - t_lo) {
-    const int nbh = p.B * p.Hkv;
-    const long u = t_lo + slot;
-    const int chunk = (int)(u / nbh), bh = (int)(u % nbh);
-    tail_unit<D, GEN>(p, bh / p.Hkv, bh % p.Hkv, chunk, reinterpret_cast<float*>(smem));
-    return;
-  }
-  const long s2 = slot - (t_hi - t_lo);
-  if (s2 >= c_hi - c_lo) return;
+  if (slot >= c_hi - c_lo) return;
   const int nbq = p.B * p.n_hq;
-  const long u = c_lo + s2;
+  const long u = c_lo + slot;
   const int j = (int)(u / nbq), bq = (int)(u % nbq);
   if constexpr (GEN) {
-    if (p.rope_mode != SC_ROPE_NONE && !p.halves_equal) {
-      cold_unit<D, KK, KV, TPW, GEN, false>(p, bq / p.n_hq, bq % p.n_hq, j, smem);
-      return;
-    }
+    if (p.rope_mode != SC_ROPE_NONE && !p.halves_equal)
+      cold_unit<D, KK, KV, TPW, GEN, false, 2>(p, bq / p.n_hq, bq % p.n_hq, j, smem);
+    else
+      cold_unit<D, KK, KV, TPW, GEN, true, 2>(p, bq / p.n_hq, bq % p.n_hq, j, smem);
+  } else {
+    if (p.per_row)
+      cold_unit<D, KK, KV, TPW, GEN, true, 1>(p, bq / p.n_hq, bq % p.n_hq, j, smem);
+    else
+      cold_unit<D, KK, KV, TPW, GEN, true, 0>(p, bq / p.n_hq, bq % p.n_hq, j, smem);
   }
-  cold_unit<D, KK, KV, TPW, GEN, true>(p, bq / p.n_hq, bq % p.n_hq, j, smem);
 }
 
 // Log-sum-exp merge of the partial records of one (sequence, query head):
@@ -1031,11 +1010,15 @@ int fill_params(const ScDecodeArgs* a, DecodeParams* p) {
   p->grid_blocks = a->grid_blocks;
   p->tpw = tpw;
   p->n_hq = (t->kv_heads + kWaves - 1) / kWaves;
-  p->cold_units = p->grid_blocks;
-  p->tail_units = (a->grid_tail + kTailUnit - 1) / kTailUnit;
-  p->units_per_bh = p->cold_units + p->tail_units;
-  p->n_cold_units = (long)p->grid_blocks * p->B * p->n_hq;
-  p->n_tail_units = (long)p->tail_units * p->B * p->Hkv;
+  // The FP16 tail is processed by the cold workgroups: tail tile t (16
+  // tokens) goes to workgroup t mod W of its sequence and head group, with
+  // W = max(grid_blocks, tail tiles): workgroups past the cold blocks only
+  // do tail work, and no workgroup gets more than one tail tile.
+  const int tail_tiles_grid = (a->grid_tail + kTile - 1) / kTile;
+  p->fold_tail = a->grid_tail > 0;
+  p->cold_units = p->grid_blocks > tail_tiles_grid ? p->grid_blocks : tail_tiles_grid;
+  p->units_per_bh = p->cold_units;
+  p->n_cold_units = (long)p->cold_units * p->B * p->n_hq;
   p->scale = a->scale;
   p->q = (const h16*)a->q;
   p->q_sb = a->q_stride_b;
@@ -1077,9 +1060,8 @@ template <int D, int KK, int KV, int TPW, bool GEN>
 int launch(DecodeParams& p, hipStream_t s) {
   long slots = 0;
   for (int x = 0; x < 8; ++x) {
-    const long nt = (x + 1) * p.n_tail_units / 8 - x * p.n_tail_units / 8;
     const long nc = (x + 1) * p.n_cold_units / 8 - x * p.n_cold_units / 8;
-    if (nt + nc > slots) slots = nt + nc;
+    if (nc > slots) slots = nc;
   }
   const long grid = 8 * slots;
   size_t lds = 0;
@@ -1087,11 +1069,9 @@ int launch(DecodeParams& p, hipStream_t s) {
     const bool he = !GEN || p.halves_equal;
     lds = (size_t)2 * kTile * TPW * (he ? RopeStage<D, true>::ROW : RopeStage<D, false>::ROW);
   }
-  if (p.tail_units > 0) {
-    const size_t merge_tail = (size_t)(2 * kWaves * p.nrep + kWaves * p.nrep * D + p.nrep * D + 2 * p.nrep) * 4;
-    const size_t stage_tail = (size_t)kWaves * kTailTiles * kTile * kVRow * 2;
-    if (merge_tail > lds) lds = merge_tail;
-    if (stage_tail > lds) lds = stage_tail;
+  if (p.fold_tail) {
+    const size_t stage_fold = (size_t)kWaves * kTile * kVRow * 2;  // one V tile per wave
+    if (stage_fold > lds) lds = stage_fold;
   }
   if (grid > 0) {
     hipLaunchKernelGGL((decode_partial_kernel<D, KK, KV, TPW, GEN>), dim3((unsigned)grid), dim3(kThreads), lds, s, p);
