@@ -1,6 +1,8 @@
 """Benchmark: spectral decode attention (C3) + rSVD block compression (C2) on one MI355X.
 
     python bench.py [--gpus 1] [--steps K] [--warmup W] [--no-cpu] [--rotate R]
+    python bench.py ... --copy-probe-mib 256          (under rocprofv3 --pmc: calibration kernel)
+    python bench.py --summarize-pmc FETCH_DIR WRITE_DIR --copy-probe-mib 256
 
 Workloads (synthetic data, seeds fixed):
   decode  batch 8, context 16384 = 31 cold 512-token blocks (INT8 codes k=32,
@@ -211,12 +213,78 @@ def cpu_rsvd_baseline(M_gpu):
                                       f"per-row quantise, 8x512x128, k=16; best of 5 ({best * 1e3:.2f} ms)"}
 
 
+TRAFFIC_JSON = os.path.join(HERE, "profiles", "decode_c3_traffic.json")
+
+
 def load_traffic():
-    path = os.path.join(HERE, "profiles", "decode_c3_traffic.json")
-    if not os.path.exists(path):
+    if not os.path.exists(TRAFFIC_JSON):
         return None
-    with open(path) as f:
+    with open(TRAFFIC_JSON) as f:
         return json.load(f).get("hbm_bytes_per_call")
+
+
+def copy_probe(torch, device, mib, reps=5):
+    """A plain streaming kernel of known size for counter calibration:
+    torch.neg over mib MiB of fp16 reads mib MiB and writes mib MiB."""
+    src = torch.ones(mib << 19, dtype=torch.float16, device=device)
+    dst = torch.empty_like(src)
+    for _ in range(reps):
+        torch.neg(src, out=dst)
+    torch.cuda.synchronize()
+    del src, dst
+
+
+def _pmc_means(path):
+    """Mean value per dispatch of every counter, per kernel name, from the
+    rocpd databases a rocprofv3 --pmc run wrote under path."""
+    import collections
+    import glob
+    import sqlite3
+    agg = collections.defaultdict(lambda: collections.defaultdict(list))
+    for db in glob.glob(os.path.join(path, "**", "*_results.db"), recursive=True):
+        con = sqlite3.connect(db)
+        cur = con.cursor()
+        cols = [r[1] for r in cur.execute("pragma table_info(counters_collection)")]
+        ci = {c: i for i, c in enumerate(cols)}
+        name_k = "kernel_name" if "kernel_name" in ci else "name"
+        for r in cur.execute("select * from counters_collection"):
+            agg[r[ci[name_k]]][r[ci["counter_name"]]].append(r[ci["value"]])
+        con.close()
+    return {k: {c: sum(v) / len(v) for c, v in d.items()} for k, d in agg.items()}
+
+
+def summarize_pmc(fetch_dir, write_dir, mib):
+    """HBM traffic of one decode call from two rocprofv3 --pmc runs of this
+    script (FETCH_SIZE, then WRITE_SIZE; KiB per dispatch), each scaled by
+    what the same counter reads for the copy probe of mib MiB."""
+    fetch, write = _pmc_means(fetch_dir), _pmc_means(write_dir)
+
+    def pick(tab, key, counter):
+        vals = {k: v[counter] for k, v in tab.items() if key in k and counter in v}
+        if not vals:
+            raise SystemExit(f"no kernel matching {key!r} with {counter}")
+        if len(vals) > 1:  # the largest dispatch is the one of interest (the copy probe)
+            print(f"{len(vals)} kernels match {key!r}: " + "; ".join(f"{k[:90]} = {v:.1f}" for k, v in vals.items()),
+                  file=sys.stderr)
+        return max(vals.values())
+
+    kib = mib * 1024.0
+    f_copy, w_copy = pick(fetch, "neg_kernel", "FETCH_SIZE"), pick(write, "neg_kernel", "WRITE_SIZE")
+    f_factor, w_factor = kib / f_copy, kib / w_copy
+    parts = {}
+    for key in ("decode_partial_kernel", "decode_combine_kernel"):
+        f, w = pick(fetch, key, "FETCH_SIZE"), pick(write, key, "WRITE_SIZE")
+        parts[key] = {"fetch_kib_raw": round(f, 1), "write_kib_raw": round(w, 1),
+                      "hbm_bytes": int(round((f * f_factor + w * w_factor) * 1024))}
+    total = sum(v["hbm_bytes"] for v in parts.values())
+    nb = decode_bytes(B, HKV, NBLK, K_RANK, K_RANK, TAIL)
+    out = {"hbm_bytes_per_call": total, "algorithmic_bytes_per_call": nb,
+           "traffic_over_algorithmic": round(total / nb, 4), "kernels": parts,
+           "copy_probe": {"mib": mib, "fetch_kib_raw": round(f_copy, 1), "write_kib_raw": round(w_copy, 1),
+                          "fetch_factor": round(f_factor, 5), "write_factor": round(w_factor, 5)}}
+    with open(TRAFFIC_JSON, "w") as f:
+        json.dump(out, f, indent=1)
+    print(json.dumps(out))
 
 
 def main():
@@ -226,10 +294,17 @@ def main():
     ap.add_argument("--warmup", type=int, default=20)
     ap.add_argument("--rotate", type=int, default=4)
     ap.add_argument("--no-cpu", action="store_true")
+    ap.add_argument("--copy-probe-mib", type=int, default=0,
+                    help="run a plain copy kernel of this size first (counter calibration)")
+    ap.add_argument("--summarize-pmc", nargs=2, metavar=("FETCH_DIR", "WRITE_DIR"),
+                    help="write the decode traffic JSON from two rocprofv3 --pmc runs and exit")
     args = ap.parse_args()
+    if args.summarize_pmc:
+        summarize_pmc(*args.summarize_pmc, args.copy_probe_mib)
+        return
     if args.gpus != 1:
         print(json.dumps({"error": "this benchmark runs on one GPU only: the spectral decode path has no "
-                                   "multi-GPU collective in this build (see DESIGN.md for how it would shard)",
+                                   "multi-GPU collective; --gpus must be 1",
                           "n_gpus": args.gpus}))
         sys.exit(2)
     import torch
@@ -238,6 +313,8 @@ def main():
     torch.cuda.set_device(device)
     lib = _lib.load()
     hip = Hip()
+    if args.copy_probe_mib:
+        copy_probe(torch, device, args.copy_probe_mib)
 
     cache0, raw = build_c3(torch, device)
     del raw

@@ -1,6 +1,6 @@
 """CPU restatement of unsloth-spectral's compressed-space decode path.
 
-THIS PACKAGE IS TEST INFRASTRUCTURE (the checker), NOT THE PRODUCT.
+THIS PACKAGE IS TEST INFRASTRUCTURE, NOT THE PRODUCT.
 Only ``tests/``, ``__graft_entry__.smoke()`` and the ``cpu_baseline`` leg of
 ``bench.py`` may import it, and only to check or time the reference
 algorithm.  The shipped path (``unsloth_spectral`` + ``libspectral_hip.so``)

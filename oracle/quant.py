@@ -13,7 +13,7 @@ Arithmetic that fixes bit-exactness (all float32):
   scale  = absmax / float32(127.0)        (:505, IEEE division)
   code   = round_half_even(x / scale)     (:508, IEEE division, torch.round)
 The per-row granularity uses the same formula with one scale per row (the
-layout BASELINE configs ask for; it has no reference counterpart).
+layout of the benchmark workloads; it has no reference counterpart).
 """
 import numpy as np
 

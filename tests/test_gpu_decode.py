@@ -1,6 +1,6 @@
 """Decode-attention parity: HIP kernel (through the C ABI) vs the oracle.
 
-Bar (BASELINE north star): outputs within 2e-3 max-abs and 1e-2 of max|ref|
+Bar: outputs within 2e-3 max-abs and 1e-2 of max|ref|
 (FP16 out, FP32 accumulate), logits Pearson >= 0.9999 against the
 FP16-faithful restatement of the same RoPE mode."""
 import zlib

@@ -1,6 +1,6 @@
 """rSVD block compressor: HIP kernel vs the oracle on the same Omega.
 
-Bar (BASELINE north star): reconstruction error within 1% (relative) of the
+Bar: reconstruction error within 1% (relative) of the
 reference for the same Omega.  The reference evaluates the sketch subspace
 in float32 without re-orthonormalisation; the kernel evaluates the same
 subspace stably, so it is compared tightly with the float64 evaluation of
