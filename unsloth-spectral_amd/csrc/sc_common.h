@@ -56,6 +56,16 @@ __device__ __forceinline__ float sum_over_rows(float v) {
   auto b = __builtin_amdgcn_permlane16_swap(w, w, false, false);
   return __uint_as_float(b[0]) + __uint_as_float(b[1]);
 }
+// Reductions over the four lanes of a quad (lanes 4k .. 4k+3) with DPP
+// quad permutes: [1,0,3,2] (0xB1) then [2,3,0,1] (0x4E).
+__device__ __forceinline__ float quad_max(float v) {
+  v = fmaxf(v, __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), 0xB1, 0xF, 0xF, false)));
+  return fmaxf(v, __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), 0x4E, 0xF, 0xF, false)));
+}
+__device__ __forceinline__ float quad_sum(float v) {
+  v += __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), 0xB1, 0xF, 0xF, false));
+  return v + __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), 0x4E, 0xF, 0xF, false));
+}
 __device__ __forceinline__ float wave_max(float v) {
 #pragma unroll
   for (int o = 32; o > 0; o >>= 1) v = fmaxf(v, __shfl_xor(v, o));

@@ -168,18 +168,17 @@ __device__ __forceinline__ void unrotated(const Half8s<Geo<D>::NV>& x1, const Ha
   }
 }
 
-// Query operand of the score MFMA: lane (g, n) holds head n, d-slots of
-// K-step s = the lane group's RoPE pairs, matching the Y layout.
+// Query operand of the score MFMA: lane (g, n) holds query head qh of the
+// group (its MFMA column), d-slots of K-step s = the lane group's RoPE
+// pairs, matching the Y layout.
 template <int D>
-__device__ __forceinline__ void load_q(const DecodeParams& p, int b, int h, int g, int n, bool hv,
-                                       half8_t (&qb)[Geo<D>::DS]) {
+__device__ __forceinline__ void load_q(const DecodeParams& p, int b, int h, int g, int qh, half8_t (&qb)[Geo<D>::DS]) {
   using G = Geo<D>;
-  const h16* qrow = p.q + b * p.q_sb + (long)(h * p.nrep + (hv ? n : 0)) * p.q_sh;
+  const h16* qrow = p.q + b * p.q_sb + (long)(h * p.nrep + qh) * p.q_sh;
 #pragma unroll
   for (int s = 0; s < G::DS; ++s) {
     const int d0 = (s < G::NV) ? g * G::QG + 8 * s : G::HALF + g * G::QG + 8 * (s - G::NV);
-    const half8_t v = *reinterpret_cast<const half8_t*>(qrow + d0);
-    qb[s] = hv ? v : (half8_t)(h16)0;
+    qb[s] = *reinterpret_cast<const half8_t*>(qrow + d0);
   }
 }
 
@@ -187,42 +186,7 @@ __device__ __forceinline__ float* record_ptr(const DecodeParams& p, int b, int h
   return p.ws + ((((long)(b * p.Hkv + h) * p.units_per_bh + unit) * p.nrep + hh) * prec);
 }
 
-__device__ __forceinline__ void write_empty(const DecodeParams& p, int b, int h, int unit, int prec) {
-  if ((int)threadIdx.x < p.nrep) {
-    float* r = record_ptr(p, b, h, unit, threadIdx.x, prec);
-    r[0] = -INFINITY;
-    r[1] = 0.f;
-  }
-}
-
 __device__ __forceinline__ int clamp_angle(int phi, int len) { return min(max(phi, 0), len - 1); }
-
-// ds_swizzle bitmask mode: lane l reads lane (l & 0x30) | SRC of its 32-lane
-// half, i.e. lane SRC of its own 16-lane row.
-template <int SRC>
-__device__ __forceinline__ float row_bcast_c(float v) {
-  return __int_as_float(__builtin_amdgcn_ds_swizzle(__float_as_int(v), 0x10 | (SRC << 5)));
-}
-__device__ __forceinline__ float row_bcast(float v, int src) {
-  switch (src) {
-    case 0: return row_bcast_c<0>(v);
-    case 1: return row_bcast_c<1>(v);
-    case 2: return row_bcast_c<2>(v);
-    case 3: return row_bcast_c<3>(v);
-    case 4: return row_bcast_c<4>(v);
-    case 5: return row_bcast_c<5>(v);
-    case 6: return row_bcast_c<6>(v);
-    case 7: return row_bcast_c<7>(v);
-    case 8: return row_bcast_c<8>(v);
-    case 9: return row_bcast_c<9>(v);
-    case 10: return row_bcast_c<10>(v);
-    case 11: return row_bcast_c<11>(v);
-    case 12: return row_bcast_c<12>(v);
-    case 13: return row_bcast_c<13>(v);
-    case 14: return row_bcast_c<14>(v);
-    default: return row_bcast_c<15>(v);
-  }
-}
 
 // The reference rounds scores and logits to the model dtype (fp16) before
 // the fp32 softmax: s = fp16(raw) (kernels/spectral_attention.py:446,
@@ -289,21 +253,22 @@ __device__ __forceinline__ Half8s<Geo<D>::NV> lds_rope(const char* smem, int row
 }
 
 // INT8 codes and scales of one wave's range (16 TPW tokens of one head).
-// sk[i] / sv[i]: the row scales of the four tokens a lane's score slots
-// hold in tile i (one 16-byte load per lane; the 16 lanes of a row share it).
-template <int KK, int KV, int TPW>
+// ONE (one logit per lane): sk[i] / sv[i] hold the row scale of the token
+// whose logit the lane holds in tile i.  Otherwise float4: the row scales
+// of the four tokens of the lane's score slots (one 16-byte load).
+template <int KK, int KV, int TPW, bool ONE>
 struct CodeBuf {
   static constexpr int NGRP = TPW / 4, NT = KV / 16, KC = KK >= 32 ? KK / 32 : 1;
   using CodeK = typename std::conditional<KK == 16, uint32_t, uint2>::type;
+  using Scale = typename std::conditional<ONE, float, float4_t>::type;
   CodeK kc[TPW][KC];
   uint4 vc[NGRP][NT];
-  float4_t sk[TPW], sv[TPW];
+  Scale sk[TPW], sv[TPW];
 };
 
-// Loads of one wave's codes (range starting at block token tok0).  Each
+// Sources of one wave's range (range starting at block token tok0).  Each
 // part can be issued on its own so that a register is refilled with the
 // next range's data right after its last use.
-template <int KK, int KV, int TPW>
 struct CodeSrc {
   const int8_t* ck;   // K codes of the range
   const int8_t* cv;   // V codes of the range
@@ -311,9 +276,9 @@ struct CodeSrc {
   const float* svp;
 };
 
-template <int KK, int KV, int TPW>
-__device__ __forceinline__ CodeSrc<KK, KV, TPW> code_src(const DecodeParams& p, long bhj, int tok0) {
-  CodeSrc<KK, KV, TPW> s;
+template <int KK, int KV>
+__device__ __forceinline__ CodeSrc code_src(const DecodeParams& p, long bhj, int tok0) {
+  CodeSrc s;
   s.ck = p.codes_k + bhj * (long)p.TB * KK + (long)tok0 * KK;
   s.cv = p.codes_v + bhj * (long)KV * p.TB + tok0;
   s.skp = p.scales_k + (p.per_row ? bhj * p.TB + tok0 : bhj);
@@ -321,9 +286,8 @@ __device__ __forceinline__ CodeSrc<KK, KV, TPW> code_src(const DecodeParams& p, 
   return s;
 }
 
-template <int KK, int KV, int TPW>
-__device__ __forceinline__ void load_kc(const CodeSrc<KK, KV, TPW>& s, int i, CodeBuf<KK, KV, TPW>& cb) {
-  using CB = CodeBuf<KK, KV, TPW>;
+template <int KK, class CB>
+__device__ __forceinline__ void load_kc(const CodeSrc& s, int i, CB& cb) {
   const int lane = threadIdx.x & 63, g = lane >> 4, n = lane & 15;
   const int tt = (i / 4) * 64 + 16 * (n >> 2) + 4 * (i % 4) + (n & 3);
 #pragma unroll
@@ -335,48 +299,98 @@ __device__ __forceinline__ void load_kc(const CodeSrc<KK, KV, TPW>& s, int i, Co
   }
 }
 
-template <int KK, int KV, int TPW>
-__device__ __forceinline__ void load_vc(const DecodeParams& p, const CodeSrc<KK, KV, TPW>& s, int gr,
-                                        CodeBuf<KK, KV, TPW>& cb) {
-  using CB = CodeBuf<KK, KV, TPW>;
+template <class CB>
+__device__ __forceinline__ void load_vc(const DecodeParams& p, const CodeSrc& s, int gr, CB& cb) {
   const int lane = threadIdx.x & 63, g = lane >> 4, n = lane & 15;
 #pragma unroll
   for (int nt = 0; nt < CB::NT; ++nt)
     cb.vc[gr][nt] = *reinterpret_cast<const uint4*>(s.cv + (long)(nt * 16 + n) * p.TB + gr * 64 + 16 * g);
 }
 
-// Row scales of tokens 64 (i / 4) + 16 g + 4 (i % 4) + {0..3} of the range
-// (per row), or the block's scale four times (per head).  PRM: 0 per head,
-// 1 per row, 2 decided at run time (general path).
-template <int PRM>
-__device__ __forceinline__ float4_t load_scale4(const DecodeParams& p, const float* base, int i) {
-  const int g = (threadIdx.x & 63) >> 4;
-  if (PRM == 1 || (PRM == 2 && p.per_row))
-    return *reinterpret_cast<const float4_t*>(base + 64 * (i / 4) + 16 * g + 4 * (i % 4));
-  return (float4_t)base[0];
+// Row scale(s) for tile i of a range: tile i covers range tokens
+// 64 (i / 4) + 16 g + 4 (i % 4) + {0..3} in lane group g, and a ONE lane
+// holds token ... + (n & 3).  Per head: the block's scale.  PRM: 0 per
+// head, 1 per row, 2 decided at run time (general path).
+template <int PRM, bool ONE>
+__device__ __forceinline__ typename std::conditional<ONE, float, float4_t>::type load_scale(const DecodeParams& p,
+                                                                                            const float* base, int i) {
+  const int lane = threadIdx.x & 63, g = lane >> 4, n = lane & 15;
+  const int t = 64 * (i / 4) + 16 * g + 4 * (i % 4);
+  const bool row = PRM == 1 || (PRM == 2 && p.per_row);
+  if constexpr (ONE) {
+    return row ? base[t + (n & 3)] : base[0];
+  } else {
+    if (row) return *reinterpret_cast<const float4_t*>(base + t);
+    return (float4_t)base[0];
+  }
 }
 
-template <int KK, int KV, int TPW, int PRM>
-__device__ __forceinline__ void load_codes(const DecodeParams& p, const CodeSrc<KK, KV, TPW>& s,
-                                           CodeBuf<KK, KV, TPW>& cb) {
-  using CB = CodeBuf<KK, KV, TPW>;
+template <int KK, int PRM, bool ONE, class CB>
+__device__ __forceinline__ void load_codes(const DecodeParams& p, const CodeSrc& s, CB& cb) {
 #pragma unroll
-  for (int i = 0; i < TPW; ++i) load_kc<KK, KV, TPW>(s, i, cb);
+  for (int i = 0; i < CB::NGRP * 4; ++i) load_kc<KK>(s, i, cb);
 #pragma unroll
-  for (int gr = 0; gr < CB::NGRP; ++gr) load_vc<KK, KV, TPW>(p, s, gr, cb);
+  for (int gr = 0; gr < CB::NGRP; ++gr) load_vc(p, s, gr, cb);
 #pragma unroll
-  for (int i = 0; i < TPW; ++i) {
-    cb.sk[i] = load_scale4<PRM>(p, s.skp, i);
-    cb.sv[i] = load_scale4<PRM>(p, s.svp, i);
+  for (int i = 0; i < CB::NGRP * 4; ++i) {
+    cb.sk[i] = load_scale<PRM, ONE>(p, s.skp, i);
+    cb.sv[i] = load_scale<PRM, ONE>(p, s.svp, i);
   }
 }
 
 // Running state of one wave (one KV head) across the ranges of a block.
 template <int KV>
 struct ColdState {
-  float m2, l;  // running max (log2 domain, per head = lane column) and lane-partial sum
+  float m2, l;  // running max (log2 domain, per head) and lane-partial sum
   float4_t pacc[KV / 16];
 };
+
+// Lane roles of the two score layouts.  The score MFMA leaves lane (g, n)
+// with tokens 4 g + {0..3} of query column n.
+//   ONE = false: column n is query head n (n < nrep); a lane holds four
+//                logits, one per token.
+//   ONE = true:  column n holds head n >> 2 (each head four times, nrep <= 4)
+//                and the lane keeps only token 4 g + (n & 3): one logit per
+//                lane, so exp2, scaling and rounding run once per
+//                (token, head).  The P operand of P.V is gathered back from
+//                the lane's quad (lanes 4 (n >> 2) + {0..3}).
+struct Lanes {
+  bool b0, b1;    // bits 0 and 1 of n: which of the four tokens a ONE lane keeps
+  bool valid;     // ONE: head n >> 2 exists (< nrep); else n < nrep
+  uint32_t psel;  // v_perm selector ordering a quad pair by quad-lane index
+};
+template <bool ONE>
+__device__ __forceinline__ Lanes lane_roles(int n, int nrep) {
+  Lanes r;
+  r.b0 = n & 1;
+  r.b1 = (n >> 1) & 1;
+  r.valid = ONE ? (n >> 2) < nrep : n < nrep;
+  r.psel = (n & 1) ? 0x05040100u : 0x01000504u;
+  return r;
+}
+
+// P values of the four lanes of this lane's quad, in quad-lane order: the
+// fp16 B operand (tokens 4 g + {0..3}) of a 16x16x16 P.V MFMA.
+__device__ __forceinline__ half4_t quad_gather_h4(float v, uint32_t psel) {
+  const uint32_t x = (uint32_t)__builtin_bit_cast(uint16_t, (h16)v);
+  const uint32_t y = (uint32_t)__builtin_amdgcn_update_dpp(0, (int)x, 0xB1, 0xF, 0xF, false);  // lane ^ 1
+  const uint32_t pair = __builtin_amdgcn_perm(x, y, psel);  // (even, odd) quad lane of this pair
+  const uint32_t lo = (uint32_t)__builtin_amdgcn_update_dpp(0, (int)pair, 0x00, 0xF, 0xF, false);  // quad lane 0
+  const uint32_t hi = (uint32_t)__builtin_amdgcn_update_dpp(0, (int)pair, 0xAA, 0xF, 0xF, false);  // quad lane 2
+  return __builtin_bit_cast(half4_t, make_uint2(lo, hi));
+}
+
+__device__ __forceinline__ float pick4(const float4_t& v, const Lanes& r) {
+  const float a = r.b0 ? v[1] : v[0], c = r.b0 ? v[3] : v[2];
+  return r.b1 ? c : a;
+}
+
+// Maximum over the lanes holding one query head's logits, in the log2 domain.
+template <bool ONE>
+__device__ __forceinline__ float head_max(float v) {
+  v = max_over_rows(v);
+  return ONE ? quad_max(v) : v;
+}
 
 // Scores (phase A), one maximum (B), probabilities and P . C_V (C) of one
 // range, merged into the running state.  If another range follows (MORE),
@@ -385,19 +399,19 @@ struct ColdState {
 // its data (nsrc) right after its last use, so the next range's HBM loads
 // are in flight during this one.  MORE and PRM are compile-time so that the
 // tile loop has no branches and the compiler can overlap tiles.
-template <int D, int KK, int KV, int TPW, bool GEN, bool HE, int PRM, bool MORE>
-__device__ __forceinline__ void cold_range(const DecodeParams& p, CodeBuf<KK, KV, TPW>& cb,
-                                           const CodeSrc<KK, KV, TPW> nsrc,
-                                           const half8_t (&a8)[Geo<D>::MT][CodeBuf<KK, KV, TPW>::KC],
+template <int D, int KK, int KV, int TPW, bool GEN, bool HE, int PRM, bool MORE, class CB>
+__device__ __forceinline__ void cold_range(const DecodeParams& p, CB& cb, const CodeSrc nsrc,
+                                           const half8_t (&a8)[Geo<D>::MT][CB::KC],
                                            const half4_t (&a4)[Geo<D>::MT], const half8_t (&qb)[Geo<D>::DS],
                                            const char* rope_cur, char* rope_next, int next_pos0, int qp, bool dist,
                                            bool rope, float vn, const uint8_t* mrow, float* lrow,
                                            ColdState<KV>& st) {
   using G = Geo<D>;
-  using CB = CodeBuf<KK, KV, TPW>;
   using RS = RopeStage<D, HE>;
+  constexpr bool ONE = !GEN;
   constexpr int NSTG = (TPW * kTile) * RS::CH / kThreads;  // staged chunks per thread
   const int lane = threadIdx.x & 63, g = lane >> 4, n = lane & 15;
+  const Lanes lr = lane_roles<ONE>(n, p.nrep);
   const bool stage = MORE && rope;
   // The next range's RoPE rows (L2 hits) are requested before any of this
   // range's HBM refills: vmcnt retires in order, so waiting for them before
@@ -412,21 +426,22 @@ __device__ __forceinline__ void cold_range(const DecodeParams& p, CodeBuf<KK, KV
       sd[k] = sc.dst;
     }
   }
-  half4_t lg[TPW];
+  half4_t lg[ONE ? 1 : TPW];  // ONE = false: four logits per tile
+  float lg1[ONE ? TPW : 1];   // ONE = true: one logit per tile
 #pragma unroll
   for (int i = 0; i < TPW; ++i) {
     const int gr = i / 4, ii = i % 4;
     float4_t x[G::MT];
     if constexpr (KK == 16) {
       const half4_t bc = i8x4_to_h4(cb.kc[i][0]);
-      if constexpr (MORE) load_kc<KK, KV, TPW>(nsrc, i, cb);
+      if constexpr (MORE) load_kc<KK>(nsrc, i, cb);
 #pragma unroll
       for (int mt = 0; mt < G::MT; ++mt) x[mt] = mfma_16x16x16(a4[mt], bc, (float4_t)0.f);
     } else {
       half8_t bc[CB::KC];
 #pragma unroll
       for (int c = 0; c < CB::KC; ++c) bc[c] = i8x8_to_h8(cb.kc[i][c]);
-      if constexpr (MORE) load_kc<KK, KV, TPW>(nsrc, i, cb);
+      if constexpr (MORE) load_kc<KK>(nsrc, i, cb);
 #pragma unroll
       for (int mt = 0; mt < G::MT; ++mt) {
         float4_t acc = (float4_t)0.f;
@@ -458,18 +473,24 @@ __device__ __forceinline__ void cold_range(const DecodeParams& p, CodeBuf<KK, KV
     float4_t sacc = (float4_t)0.f;
 #pragma unroll
     for (int s = 0; s < G::DS; ++s) sacc = mfma_16x16x32(ya[s], qb[s], sacc);
-    // lane holds head n, range tokens tg + jj, tg = 64 gr + 16 g + 4 ii
-    const int tg = gr * 64 + 16 * g + 4 * ii;
+    if constexpr (ONE) {
+      const float l = (float)fp16_logit(pick4(sacc, lr) * cb.sk[i], p.scale);
+      lg1[i] = lr.valid ? l : -INFINITY;
+      if constexpr (MORE) cb.sk[i] = load_scale<PRM, ONE>(p, nsrc.skp, i);
+    } else {
+      // lane holds head n, range tokens tg + jj, tg = 64 gr + 16 g + 4 ii
+      const int tg = gr * 64 + 16 * g + 4 * ii;
 #pragma unroll
-    for (int jj = 0; jj < 4; ++jj) lg[i][jj] = fp16_logit(sacc[jj] * cb.sk[i][jj], p.scale);
-    if constexpr (MORE) cb.sk[i] = load_scale4<PRM>(p, nsrc.skp, i);
-    if constexpr (GEN) {
-      uint32_t keep = 0xffffffffu;
-      if (mrow) keep = *reinterpret_cast<const uint32_t*>(mrow + tg);
+      for (int jj = 0; jj < 4; ++jj) lg[i][jj] = fp16_logit(sacc[jj] * cb.sk[i][jj], p.scale);
+      if constexpr (MORE) cb.sk[i] = load_scale<PRM, ONE>(p, nsrc.skp, i);
+      if constexpr (GEN) {
+        uint32_t keep = 0xffffffffu;
+        if (mrow) keep = *reinterpret_cast<const uint32_t*>(mrow + tg);
 #pragma unroll
-      for (int jj = 0; jj < 4; ++jj) {
-        if (lrow) lrow[tg + jj] = (float)lg[i][jj];
-        if (!((keep >> (8 * jj)) & 0xffu)) lg[i][jj] = (h16)(-INFINITY);
+        for (int jj = 0; jj < 4; ++jj) {
+          if (lrow) lrow[tg + jj] = (float)lg[i][jj];
+          if (!((keep >> (8 * jj)) & 0xffu)) lg[i][jj] = (h16)(-INFINITY);
+        }
       }
     }
   }
@@ -480,7 +501,16 @@ __device__ __forceinline__ void cold_range(const DecodeParams& p, CodeBuf<KK, KV
     }
   }
   // ---- B. range maximum, merged into the running maximum
-  const float mr = max_over_rows(lane_max_log2<TPW>(lg));
+  float mloc;
+  if constexpr (ONE) {
+    mloc = lg1[0];
+#pragma unroll
+    for (int i = 1; i < TPW; ++i) mloc = fmaxf(mloc, lg1[i]);
+    mloc *= kLog2e;
+  } else {
+    mloc = lane_max_log2<TPW>(lg);
+  }
+  const float mr = head_max<ONE>(mloc);
   const float m_new = fmaxf(st.m2, mr);
   const float msub = (m_new == -INFINITY) ? 0.f : m_new;
   const float alpha = fast_exp2(st.m2 - msub);  // exp2(-inf) = 0 on the first range
@@ -492,15 +522,22 @@ __device__ __forceinline__ void cold_range(const DecodeParams& p, CodeBuf<KK, KV
 #pragma unroll
   for (int i = 0; i < TPW; ++i) {
     const int gr = i / 4, ii = i % 4;
-    float pv[4];
+    half4_t pb;
+    if constexpr (ONE) {
+      const float pv = fast_exp2(__builtin_fmaf(lg1[i], kLog2e, -msub));
+      st.l += pv;
+      pb = quad_gather_h4(pv * cb.sv[i] * vn, lr.psel);
+    } else {
+      float pv[4];
 #pragma unroll
-    for (int jj = 0; jj < 4; ++jj) {
-      pv[jj] = fast_exp2(__builtin_fmaf((float)lg[i][jj], kLog2e, -msub));
-      st.l += pv[jj];
+      for (int jj = 0; jj < 4; ++jj) {
+        pv[jj] = fast_exp2(__builtin_fmaf((float)lg[i][jj], kLog2e, -msub));
+        st.l += pv[jj];
+      }
+      const float4_t svn = cb.sv[i] * vn;
+      pb = (half4_t){(h16)(pv[0] * svn[0]), (h16)(pv[1] * svn[1]), (h16)(pv[2] * svn[2]), (h16)(pv[3] * svn[3])};
     }
-    const float4_t svn = cb.sv[i] * vn;
-    const half4_t pb = {(h16)(pv[0] * svn[0]), (h16)(pv[1] * svn[1]), (h16)(pv[2] * svn[2]), (h16)(pv[3] * svn[3])};
-    if constexpr (MORE) cb.sv[i] = load_scale4<PRM>(p, nsrc.svp, i);
+    if constexpr (MORE) cb.sv[i] = load_scale<PRM, ONE>(p, nsrc.svp, i);
 #pragma unroll
     for (int nt = 0; nt < CB::NT; ++nt) {
       const uint4 w4 = cb.vc[gr][nt];
@@ -508,7 +545,7 @@ __device__ __forceinline__ void cold_range(const DecodeParams& p, CodeBuf<KK, KV
       st.pacc[nt] = mfma_16x16x16(i8x4_to_h4(word), pb, st.pacc[nt]);
     }
     if constexpr (MORE) {
-      if (ii == 3) load_vc<KK, KV, TPW>(p, nsrc, gr, cb);
+      if (ii == 3) load_vc(p, nsrc, gr, cb);
     }
   }
 }
@@ -551,17 +588,18 @@ __device__ __forceinline__ void tail_fetch(const DecodeParams& p, int b, int h, 
 // One FP16 tail tile (tokens t0 .. t0 + 15 of one KV head, loads in f),
 // merged into the wave's running softmax state.  Scores use the fp16
 // pre-RoPE keys rotated at their stored positions; P.V accumulates in oacc
-// (O^T layout: lane (g, n) holds O[head n][16 mt + 4 g + jj]).  The V tile is
-// transposed through a wave-private LDS region.
+// (O^T layout: lane (g, n) holds O[query column n][16 mt + 4 g + jj]).  The
+// V tile is transposed through a wave-private LDS region.
 template <int D, bool GEN, bool HE>
 __device__ __forceinline__ void tail_tile(const DecodeParams& p, int b, int h, int t0, int tl, int ncold,
                                           const half8_t (&qb)[Geo<D>::DS], h16* vs, TailFetch<D> f, TailState& sm,
                                           float4_t (&oacc)[Geo<D>::MT]) {
   using G = Geo<D>;
+  constexpr bool ONE = !GEN;
   constexpr int QPR = D / 32;  // 16-byte chunks per quarter of a V row
   const int lane = threadIdx.x & 63, g = lane >> 4, n = lane & 15;
   const int vr = lane >> 2, vqtr = lane & 3;
-  const bool hv = n < p.nrep;
+  const Lanes lr = lane_roles<ONE>(n, p.nrep);
   const bool rope = !GEN || p.rope_mode != SC_ROPE_NONE;
   if (t0 + n >= tl) {
 #pragma unroll
@@ -595,34 +633,54 @@ __device__ __forceinline__ void tail_tile(const DecodeParams& p, int b, int h, i
   float4_t sacc = (float4_t)0.f;
 #pragma unroll
   for (int s = 0; s < G::DS; ++s) sacc = mfma_16x16x32(ya[s], qb[s], sacc);
-  const long cache_off = (long)ncold * p.TB;  // tail follows the cold blocks in cache order
-  half4_t lg1[1];
+  half4_t pb;
+  float alpha;
+  if constexpr (ONE) {
+    const bool valid = lr.valid && t0 + 4 * g + (n & 3) < tl;
+    const float l16 = (float)fp16_logit(pick4(sacc, lr), p.scale);
+    const float lg = valid ? l16 : -INFINITY;
+    const float mt = head_max<ONE>(lg * kLog2e);
+    const float m_new = fmaxf(sm.m2, mt);
+    const float msub = (m_new == -INFINITY) ? 0.f : m_new;
+    alpha = fast_exp2(sm.m2 - msub);
+    sm.m2 = m_new;
+    sm.l *= alpha;
+    sm.scale *= alpha;  // rescale of the cold accumulators (applied by the caller)
+    const float pv = fast_exp2(__builtin_fmaf(lg, kLog2e, -msub));
+    sm.l += pv;
+    pb = quad_gather_h4(pv, lr.psel);
+  } else {
+    const long cache_off = (long)ncold * p.TB;  // tail follows the cold blocks in cache order
+    const bool hv = n < p.nrep;
+    half4_t lg1[1];
 #pragma unroll
-  for (int jj = 0; jj < 4; ++jj) {
-    const int tk = t0 + 4 * g + jj;
-    const bool valid = tk < tl;
-    h16 l16 = fp16_logit(sacc[jj], p.scale);
-    if constexpr (GEN) {
-      if (p.logits && hv && valid) p.logits[b * p.lg_sb + (long)(h * p.nrep + n) * p.lg_sh + cache_off + tk] = (float)l16;
-      if (p.mask && hv && valid && p.mask[b * p.mask_sb + (long)(h * p.nrep + n) * p.mask_sh + cache_off + tk] == 0)
-        l16 = (h16)(-INFINITY);
+    for (int jj = 0; jj < 4; ++jj) {
+      const int tk = t0 + 4 * g + jj;
+      const bool valid = tk < tl;
+      h16 l16 = fp16_logit(sacc[jj], p.scale);
+      if constexpr (GEN) {
+        if (p.logits && hv && valid)
+          p.logits[b * p.lg_sb + (long)(h * p.nrep + n) * p.lg_sh + cache_off + tk] = (float)l16;
+        if (p.mask && hv && valid && p.mask[b * p.mask_sb + (long)(h * p.nrep + n) * p.mask_sh + cache_off + tk] == 0)
+          l16 = (h16)(-INFINITY);
+      }
+      lg1[0][jj] = valid ? l16 : (h16)(-INFINITY);
     }
-    lg1[0][jj] = valid ? l16 : (h16)(-INFINITY);
-  }
-  const float mt = max_over_rows(lane_max_log2<1>(lg1));
-  const float m_new = fmaxf(sm.m2, mt);
-  const float msub = (m_new == -INFINITY) ? 0.f : m_new;
-  const float alpha = fast_exp2(sm.m2 - msub);
-  sm.m2 = m_new;
-  sm.l *= alpha;
-  sm.scale *= alpha;  // rescale of the cold accumulators (applied by the caller)
-  float pv[4];
+    const float mt = head_max<ONE>(lane_max_log2<1>(lg1));
+    const float m_new = fmaxf(sm.m2, mt);
+    const float msub = (m_new == -INFINITY) ? 0.f : m_new;
+    alpha = fast_exp2(sm.m2 - msub);
+    sm.m2 = m_new;
+    sm.l *= alpha;
+    sm.scale *= alpha;
+    float pv[4];
 #pragma unroll
-  for (int jj = 0; jj < 4; ++jj) {
-    pv[jj] = fast_exp2(__builtin_fmaf((float)lg1[0][jj], kLog2e, -msub));
-    sm.l += pv[jj];
+    for (int jj = 0; jj < 4; ++jj) {
+      pv[jj] = fast_exp2(__builtin_fmaf((float)lg1[0][jj], kLog2e, -msub));
+      sm.l += pv[jj];
+    }
+    pb = (half4_t){(h16)pv[0], (h16)pv[1], (h16)pv[2], (h16)pv[3]};
   }
-  const half4_t pb = {(h16)pv[0], (h16)pv[1], (h16)pv[2], (h16)pv[3]};
   __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
   __builtin_amdgcn_wave_barrier();
   __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
@@ -655,6 +713,33 @@ __device__ __forceinline__ void tail_tiles(const DecodeParams& p, int b, int h, 
   }
 }
 
+// Writes a wave's partial record: lane (g, n) holds o[column n][16 mt + 4 g
+// + jj]; query column n is head n (ONE = false) or head n >> 2 (ONE = true,
+// written by quad lane 0).
+template <int D, bool ONE>
+__device__ __forceinline__ void write_record(const DecodeParams& p, int b, int h, int unit, const Lanes& lr,
+                                             const float4_t (&o)[Geo<D>::MT], float m2, float l) {
+  using G = Geo<D>;
+  const int lane = threadIdx.x & 63, g = lane >> 4, n = lane & 15;
+  const bool wr = lr.valid && (!ONE || (n & 3) == 0);
+  const int hh = ONE ? n >> 2 : n;
+  float* rec = record_ptr(p, b, h, unit, wr ? hh : 0, G::PREC);
+#pragma unroll
+  for (int mt = 0; mt < G::MT; ++mt)
+    if (wr) *reinterpret_cast<float4_t*>(rec + 4 + 16 * mt + 4 * g) = o[mt];
+  if (wr && g == 0) {
+    rec[0] = m2;
+    rec[1] = l;
+  }
+}
+
+// Total of a lane-partial sum over the lanes of one query head.
+template <bool ONE>
+__device__ __forceinline__ float head_sum(float v) {
+  v = sum_over_rows(v);
+  return ONE ? quad_sum(v) : v;
+}
+
 // Unit j of (sequence b, group of four KV heads hq): wave w is KV head
 // 4 hq + w.  Cold block j (if the sequence has it) is walked in ranges of
 // T = 16 TPW tokens; the RoPE rows of a range are staged once per
@@ -665,7 +750,8 @@ __device__ __forceinline__ void tail_tiles(const DecodeParams& p, int b, int h, 
 template <int D, int KK, int KV, int TPW, bool GEN, bool HE, int PRM>
 __device__ void cold_unit(const DecodeParams& p, int b, int hq, int j, char* smem) {
   using G = Geo<D>;
-  using CB = CodeBuf<KK, KV, TPW>;
+  constexpr bool ONE = !GEN;
+  using CB = CodeBuf<KK, KV, TPW, ONE>;
   using RS = RopeStage<D, HE>;
   constexpr int T = kTile * TPW;
   constexpr int NT = KV / 16;
@@ -673,13 +759,15 @@ __device__ void cold_unit(const DecodeParams& p, int b, int hq, int j, char* sme
   const int lane = threadIdx.x & 63, w = threadIdx.x >> 6, g = lane >> 4, n = lane & 15;
   const int h = hq * kWaves + w;
   const bool hvalid = h < p.Hkv;
+  const int nrep = p.nrep;
+  const Lanes lr = lane_roles<ONE>(n, nrep);
+  const int qhead = ONE ? n >> 2 : n;  // query head of this lane's MFMA column
   const int ncold = p.counters[b * SC_NCOUNTERS + SC_CNT_NCOLD];
   if (j >= ncold) {  // uniform over the workgroup: no cold block, tail tiles only
     if (!hvalid) return;
-    const bool hv0 = n < p.nrep;
     half8_t qt[G::DS];
-    if (hv0) {
-      load_q<D>(p, b, h, g, n, true, qt);
+    if (lr.valid) {
+      load_q<D>(p, b, h, g, qhead, qt);
     } else {
 #pragma unroll
       for (int s = 0; s < G::DS; ++s) qt[s] = (half8_t)(h16)0;
@@ -701,19 +789,9 @@ __device__ void cold_unit(const DecodeParams& p, int b, int hq, int j, char* sme
       else if constexpr (GEN)
         tail_tiles<D, GEN, false>(p, b, h, j, qt, smem + w * kTile * kVRow * 2, tf, sm, oacc);
     }
-    sm.l = sum_over_rows(sm.l);
-    float* rec = record_ptr(p, b, h, j, hv0 ? n : 0, G::PREC);
-#pragma unroll
-    for (int m = 0; m < G::MT; ++m)
-      if (hv0) *reinterpret_cast<float4_t*>(rec + 4 + 16 * m + 4 * g) = oacc[m];
-    if (hv0 && g == 0) {
-      rec[0] = sm.m2;
-      rec[1] = sm.l;
-    }
+    write_record<D, ONE>(p, b, h, j, lr, oacc, sm.m2, head_sum<ONE>(sm.l));
     return;
   }
-  const int nrep = p.nrep;
-  const bool hv = n < nrep;
   const long bhj = (long)(b * p.Hkv + (hvalid ? h : 0)) * p.NB + j;
   const int start = p.block_start[b * p.NB + j];
   const int qp = p.qpos ? p.qpos[b] : p.qpos_scalar;
@@ -742,7 +820,7 @@ __device__ void cold_unit(const DecodeParams& p, int b, int hq, int j, char* sme
   half8_t qb[G::DS];
   float vn = 1.f;
   if (hvalid) {
-    load_codes<KK, KV, TPW, PRM>(p, code_src<KK, KV, TPW>(p, bhj, 0), cb0);
+    load_codes<KK, PRM, ONE>(p, code_src<KK, KV>(p, bhj, 0), cb0);
     // K basis as the A operand: row n of tile mt is d = perm(mt, n).
     const h16* bk = p.basis_k + bhj * (long)D * KK;
 #pragma unroll
@@ -756,8 +834,8 @@ __device__ void cold_unit(const DecodeParams& p, int b, int hq, int j, char* sme
         for (int c = 0; c < KC; ++c) a8[mt][c] = *reinterpret_cast<const half8_t*>(bk + d * KK + c * 32 + 8 * g);
       }
     }
-    if (hv) {
-      load_q<D>(p, b, h, g, n, true, qb);
+    if (lr.valid) {
+      load_q<D>(p, b, h, g, qhead, qb);
     } else {
 #pragma unroll
       for (int s = 0; s < G::DS; ++s) qb[s] = (half8_t)(h16)0;
@@ -768,8 +846,8 @@ __device__ void cold_unit(const DecodeParams& p, int b, int hq, int j, char* sme
   const uint8_t* mrow = nullptr;
   float* lrow = nullptr;
   if constexpr (GEN) {
-    mrow = (p.mask && hv) ? p.mask + b * p.mask_sb + (long)(h * nrep + n) * p.mask_sh + cache_tok : nullptr;
-    lrow = (p.logits && hv) ? p.logits + b * p.lg_sb + (long)(h * nrep + n) * p.lg_sh + cache_tok : nullptr;
+    mrow = (p.mask && lr.valid) ? p.mask + b * p.mask_sb + (long)(h * nrep + n) * p.mask_sh + cache_tok : nullptr;
+    lrow = (p.logits && lr.valid) ? p.logits + b * p.lg_sb + (long)(h * nrep + n) * p.lg_sh + cache_tok : nullptr;
   }
   ColdState<KV> st;
   st.m2 = -INFINITY;
@@ -784,8 +862,8 @@ __device__ void cold_unit(const DecodeParams& p, int b, int hq, int j, char* sme
     char* cur = smem + (rr & 1) * RBUF;
     char* next = smem + ((rr + 1) & 1) * RBUF;
     if (hvalid) {
-      cold_range<D, KK, KV, TPW, GEN, HE, PRM, M>(p, cb0, code_src<KK, KV, TPW>(p, bhj, (rr + 1) * T), a8, a4, qb,
-                                                   cur, next, start + (rr + 1) * T, qp, dist, rope, vn,
+      cold_range<D, KK, KV, TPW, GEN, HE, PRM, M>(p, cb0, code_src<KK, KV>(p, bhj, (rr + 1) * T), a8, a4, qb, cur,
+                                                   next, start + (rr + 1) * T, qp, dist, rope, vn,
                                                    mrow ? mrow + rr * T : nullptr, lrow ? lrow + rr * T : nullptr, st);
     } else if (M && rope) {
       // idle head slot: still stage its share of the next range's rows
@@ -825,11 +903,10 @@ __device__ void cold_unit(const DecodeParams& p, int b, int hq, int j, char* sme
 #pragma unroll
     for (int nt = 0; nt < NT; ++nt) st.pacc[nt] *= sm.scale;
   }
-  st.l = sum_over_rows(st.l);
 
-  // ---- projection O^T[d][head] = B_V^T[d][i] . Pacc[i][head] on MFMA; Pacc
-  // (coefficient i = 16 nt + 4 g + jj of head n, already the B-operand
-  // layout) is split into fp16 hi + lo parts to keep fp32 accuracy.
+  // ---- projection O^T[d][column] = B_V^T[d][i] . Pacc[i][column] on MFMA;
+  // Pacc (coefficient i = 16 nt + 4 g + jj of column n, already the
+  // B-operand layout) is split into fp16 hi + lo parts to keep fp32 accuracy.
   half4_t bvf[G::MT][NT];
   const h16* bvb = p.basis_v + bhj * (long)D * KV;
 #pragma unroll
@@ -847,21 +924,18 @@ __device__ void cold_unit(const DecodeParams& p, int b, int hq, int j, char* sme
       pl[nt][jj] = (h16)(st.pacc[nt][jj] - (float)hi);
     }
   const float ivn = 1.0f / vn;
-  float* rec = record_ptr(p, b, h, j, hv ? n : 0, G::PREC);
+  float4_t o[G::MT];
 #pragma unroll
   for (int mt = 0; mt < G::MT; ++mt) {
-    float4_t o = (float4_t)0.f;
+    float4_t acc = (float4_t)0.f;
 #pragma unroll
     for (int nt = 0; nt < NT; ++nt) {
-      o = mfma_16x16x16(bvf[mt][nt], ph[nt], o);
-      o = mfma_16x16x16(bvf[mt][nt], pl[nt], o);
+      acc = mfma_16x16x16(bvf[mt][nt], ph[nt], acc);
+      acc = mfma_16x16x16(bvf[mt][nt], pl[nt], acc);
     }
-    if (hv) *reinterpret_cast<float4_t*>(rec + 4 + 16 * mt + 4 * g) = o * ivn + oacc[mt];
+    o[mt] = acc * ivn + oacc[mt];
   }
-  if (hv && g == 0) {
-    rec[0] = st.m2;
-    rec[1] = st.l;
-  }
+  write_record<D, ONE>(p, b, h, j, lr, o, st.m2, head_sum<ONE>(st.l));
 }
 
 // Workgroup x runs on XCD x % 8 (round-robin dispatch).  Each XCD gets a
@@ -1128,7 +1202,10 @@ extern "C" int sc_decode_attn(const ScDecodeArgs* args, void* workspace, size_t 
   p.ws = (float*)workspace;
   hipStream_t s = (hipStream_t)stream;
   const int kk = args->tier->kp_keys, kv = args->tier->kp_values;
-  const bool gen = args->mask || args->logits_out || args->rope_mode == SC_ROPE_NONE || !args->halves_equal;
+  // The branch-free path keeps one logit per lane, which needs GQA groups
+  // of at most 4 query heads.
+  const bool gen = args->mask || args->logits_out || args->rope_mode == SC_ROPE_NONE || !args->halves_equal ||
+                   args->q_heads / args->tier->kv_heads > 4;
   if (D == 128)
     return gen ? dispatch_kk<128, true>(p, kk, kv, s) : dispatch_kk<128, false>(p, kk, kv, s);
   return gen ? dispatch_kk<64, true>(p, kk, kv, s) : dispatch_kk<64, false>(p, kk, kv, s);
