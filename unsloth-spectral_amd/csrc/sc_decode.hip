@@ -216,31 +216,85 @@ __device__ __forceinline__ int swap_fields(int r) { return (r & ~0x3c) | ((r & 0
 
 template <int D, bool HE>
 struct RopeStage {
-  static constexpr int HCH = D / 16;                 // 16-byte chunks per half row of one table
-  static constexpr int CH = HE ? 2 * HCH : 4 * HCH;  // cos1 | sin1 (| cos2 | sin2)
-  static constexpr int ROW = CH * 16 + 16;           // LDS row pitch in bytes
+  static constexpr int HCH = D / 16;              // 16-byte chunks per half row of one table
+  static constexpr int CHT = HE ? HCH : 2 * HCH;  // chunks of one table per staged row
+  static constexpr int CH = 2 * CHT;              // cos (1 | 2) then sin (1 | 2)
+  static constexpr int ROW = CH * 16 + 16;        // LDS row pitch in bytes
 };
 
-// Chunk k of this thread's share of a range's RoPE rows: global source and
-// LDS destination.
-template <int D, bool HE>
-struct StageChunk {
-  const uint4* src;
-  int dst;
+// Thread t stages chunk c = k * kThreads + t (k < NS) of each table for a
+// range of T rows: staged row c / CHT, table column c % CHT.  The global
+// byte offsets are relative to the range's base angle row (the same for
+// every range of a block) so that the per-range address is one scalar.
+template <int D, bool HE, int T>
+struct StageMap {
+  static constexpr int NS = T * RopeStage<D, HE>::CHT / kThreads;  // chunks per table per thread
+  uint32_t src[NS];  // byte offset of the chunk from the base angle row
+  int dst[NS];       // LDS byte offset of the cos chunk (its sin chunk follows CHT chunks later)
 };
-template <int D, bool HE>
-__device__ __forceinline__ StageChunk<D, HE> stage_chunk(const DecodeParams& p, int k, int pos0, int qp, bool dist) {
+
+template <int D, bool HE, int T>
+__device__ __forceinline__ StageMap<D, HE, T> stage_map(const DecodeParams& p, bool dist) {
   using RS = RopeStage<D, HE>;
-  const int c = k * kThreads + threadIdx.x;
-  const int r = c / RS::CH, q = c % RS::CH;
-  const int pos = pos0 + swap_fields(r);
-  const int phi = clamp_angle(dist ? max(qp - pos, 0) : pos, p.rope_len);
-  const int half = q / (2 * RS::HCH), qq = q % (2 * RS::HCH);
-  const h16* tab = qq < RS::HCH ? p.cos : p.sin;
-  StageChunk<D, HE> s;
-  s.src = reinterpret_cast<const uint4*>(tab + (long)phi * p.rope_stride + half * (D / 2) + 8 * (qq % RS::HCH));
-  s.dst = r * RS::ROW + q * 16;
-  return s;
+  StageMap<D, HE, T> m;
+#pragma unroll
+  for (int k = 0; k < StageMap<D, HE, T>::NS; ++k) {
+    const int c = k * kThreads + threadIdx.x;
+    const int r = c / RS::CHT, col = c % RS::CHT;
+    const int tok = swap_fields(r);
+    m.src[k] = (uint32_t)(((dist ? T - 1 - tok : tok) * (int)p.rope_stride + 8 * col) * 2);
+    m.dst[k] = r * RS::ROW + col * 16;
+  }
+  return m;
+}
+
+// Fetches the RoPE rows of the range starting at token position pos0:
+// angle p (absolute) or q - p (distance) of each of its T tokens.  Inside
+// the table the range is one contiguous span of rows starting at a
+// wave-uniform base; at the table edges each angle is clamped.
+template <int N>
+struct U4s {
+  uint4 v[N];
+};
+
+template <int D, bool HE, int T>
+__device__ __forceinline__ U4s<2 * StageMap<D, HE, T>::NS> stage_fetch(const DecodeParams& p,
+                                                                      const StageMap<D, HE, T>& m, int pos0, int qp,
+                                                                      bool dist) {
+  using RS = RopeStage<D, HE>;
+  constexpr int NS = StageMap<D, HE, T>::NS;
+  const int base = dist ? qp - pos0 - (T - 1) : pos0;
+  const bool inside = base >= 0 && base + T <= p.rope_len;
+  const long b0 = (long)base * p.rope_stride;
+  const char* cb = reinterpret_cast<const char*>(p.cos + b0);
+  const char* sb = reinterpret_cast<const char*>(p.sin + b0);
+  U4s<2 * NS> r;
+#pragma unroll
+  for (int k = 0; k < NS; ++k) {
+    if (inside) {
+      r.v[k] = *reinterpret_cast<const uint4*>(cb + m.src[k]);
+      r.v[NS + k] = *reinterpret_cast<const uint4*>(sb + m.src[k]);
+    } else {  // rows at the table edges: clamp each angle
+      const int c = k * kThreads + threadIdx.x;
+      const int row = c / RS::CHT, col = c % RS::CHT;
+      const int pos = pos0 + swap_fields(row);
+      const long off = (long)clamp_angle(dist ? max(qp - pos, 0) : pos, p.rope_len) * p.rope_stride + 8 * col;
+      r.v[k] = *reinterpret_cast<const uint4*>(p.cos + off);
+      r.v[NS + k] = *reinterpret_cast<const uint4*>(p.sin + off);
+    }
+  }
+  return r;
+}
+
+template <int D, bool HE, int T>
+__device__ __forceinline__ void stage_store(char* buf, const StageMap<D, HE, T>& m,
+                                            const U4s<2 * StageMap<D, HE, T>::NS>& v) {
+  constexpr int NS = StageMap<D, HE, T>::NS;
+#pragma unroll
+  for (int k = 0; k < NS; ++k) {
+    *reinterpret_cast<uint4*>(buf + m.dst[k]) = v.v[k];
+    *reinterpret_cast<uint4*>(buf + m.dst[k] + RopeStage<D, HE>::CHT * 16) = v.v[NS + k];
+  }
 }
 
 template <int D, bool HE>
@@ -286,25 +340,30 @@ __device__ __forceinline__ CodeSrc code_src(const DecodeParams& p, long bhj, int
   return s;
 }
 
+// Lane offsets are unsigned 32-bit values added to wave-uniform bases, so
+// each load is one SGPR base + VGPR offset (+ immediate) with no per-lane
+// 64-bit address arithmetic.
 template <int KK, class CB>
 __device__ __forceinline__ void load_kc(const CodeSrc& s, int i, CB& cb) {
-  const int lane = threadIdx.x & 63, g = lane >> 4, n = lane & 15;
-  const int tt = (i / 4) * 64 + 16 * (n >> 2) + 4 * (i % 4) + (n & 3);
+  const uint32_t lane = threadIdx.x & 63, g = lane >> 4, n = lane & 15;
+  const uint32_t off = (16 * (n >> 2) + (n & 3)) * KK + (KK == 16 ? 4 : 8) * g;
+  const int8_t* base = s.ck + ((i / 4) * 64 + 4 * (i % 4)) * KK;
 #pragma unroll
   for (int c = 0; c < CB::KC; ++c) {
     if constexpr (KK == 16)
-      cb.kc[i][c] = *reinterpret_cast<const uint32_t*>(s.ck + tt * KK + 4 * g);
+      cb.kc[i][c] = *reinterpret_cast<const uint32_t*>(base + off);
     else
-      cb.kc[i][c] = *reinterpret_cast<const uint2*>(s.ck + tt * KK + c * 32 + 8 * g);
+      cb.kc[i][c] = *reinterpret_cast<const uint2*>(base + c * 32 + off);
   }
 }
 
 template <class CB>
 __device__ __forceinline__ void load_vc(const DecodeParams& p, const CodeSrc& s, int gr, CB& cb) {
-  const int lane = threadIdx.x & 63, g = lane >> 4, n = lane & 15;
+  const uint32_t lane = threadIdx.x & 63, g = lane >> 4, n = lane & 15;
+  const uint32_t off = n * (uint32_t)p.TB + 16 * g;
 #pragma unroll
   for (int nt = 0; nt < CB::NT; ++nt)
-    cb.vc[gr][nt] = *reinterpret_cast<const uint4*>(s.cv + (long)(nt * 16 + n) * p.TB + gr * 64 + 16 * g);
+    cb.vc[gr][nt] = *reinterpret_cast<const uint4*>(s.cv + (long)nt * 16 * p.TB + gr * 64 + off);
 }
 
 // Row scale(s) for tile i of a range: tile i covers range tokens
@@ -314,13 +373,13 @@ __device__ __forceinline__ void load_vc(const DecodeParams& p, const CodeSrc& s,
 template <int PRM, bool ONE>
 __device__ __forceinline__ typename std::conditional<ONE, float, float4_t>::type load_scale(const DecodeParams& p,
                                                                                             const float* base, int i) {
-  const int lane = threadIdx.x & 63, g = lane >> 4, n = lane & 15;
-  const int t = 64 * (i / 4) + 16 * g + 4 * (i % 4);
+  const uint32_t lane = threadIdx.x & 63, g = lane >> 4, n = lane & 15;
+  const float* tile = base + 64 * (i / 4) + 4 * (i % 4);
   const bool row = PRM == 1 || (PRM == 2 && p.per_row);
   if constexpr (ONE) {
-    return row ? base[t + (n & 3)] : base[0];
+    return row ? tile[16 * g + (n & 3)] : base[0];
   } else {
-    if (row) return *reinterpret_cast<const float4_t*>(base + t);
+    if (row) return *reinterpret_cast<const float4_t*>(tile + 16 * g);
     return (float4_t)base[0];
   }
 }
@@ -392,42 +451,47 @@ __device__ __forceinline__ float head_max(float v) {
   return ONE ? quad_max(v) : v;
 }
 
-// Scores (phase A), one maximum (B), probabilities and P . C_V (C) of one
-// range, merged into the running state.  If another range follows (MORE),
-// its RoPE rows are fetched into registers before phase A and written to
-// the other LDS buffer after it, and every code register is refilled with
-// its data (nsrc) right after its last use, so the next range's HBM loads
-// are in flight during this one.  MORE and PRM are compile-time so that the
-// tile loop has no branches and the compiler can overlap tiles.
+// Logits of one range: one per tile (ONE) or four per tile.
+template <bool ONE, int TPW>
+struct RangeLogits {
+  typename std::conditional<ONE, float, half4_t>::type v[TPW];
+};
+
+// A range is processed in three phases: scores (A), the range maximum (B)
+// and probabilities with P . C_V (C).  Phase C of a range runs in the next
+// range's step, after that range's phase A, so that the latency chains of
+// C (exp, quad gather, accumulation) overlap A's independent work.
+
+// Phase A: scores of the range's TPW tiles.  If another range follows
+// (MORE), its RoPE rows are fetched into registers first and written to the
+// other LDS buffer at the end, and each K code and K scale register is
+// refilled from nsrc (the next range) right after its last use, so the next
+// range's HBM loads are in flight during this one.  MORE and PRM are
+// compile-time so that the tile loop has no branches.
 template <int D, int KK, int KV, int TPW, bool GEN, bool HE, int PRM, bool MORE, class CB>
-__device__ __forceinline__ void cold_range(const DecodeParams& p, CB& cb, const CodeSrc nsrc,
-                                           const half8_t (&a8)[Geo<D>::MT][CB::KC],
-                                           const half4_t (&a4)[Geo<D>::MT], const half8_t (&qb)[Geo<D>::DS],
-                                           const char* rope_cur, char* rope_next, int next_pos0, int qp, bool dist,
-                                           bool rope, float vn, const uint8_t* mrow, float* lrow,
-                                           ColdState<KV>& st) {
+__device__ __forceinline__ void range_scores(const DecodeParams& p, CB& cb, const CodeSrc nsrc,
+                                             const half8_t (&a8)[Geo<D>::MT][CB::KC],
+                                             const half4_t (&a4)[Geo<D>::MT], const half8_t (&qb)[Geo<D>::DS],
+                                             const StageMap<D, HE, kTile * TPW>& smap, const char* rope_cur,
+                                             char* rope_next, int next_pos0, int qp, bool dist, bool rope,
+                                             const uint8_t* mrow, float* lrow, RangeLogits<!GEN, TPW>& lg) {
   using G = Geo<D>;
   using RS = RopeStage<D, HE>;
   constexpr bool ONE = !GEN;
-  constexpr int NSTG = (TPW * kTile) * RS::CH / kThreads;  // staged chunks per thread
+  constexpr int T = kTile * TPW;
   const int lane = threadIdx.x & 63, g = lane >> 4, n = lane & 15;
   const Lanes lr = lane_roles<ONE>(n, p.nrep);
   const bool stage = MORE && rope;
   // The next range's RoPE rows (L2 hits) are requested before any of this
   // range's HBM refills: vmcnt retires in order, so waiting for them before
   // the LDS stores below never waits for the refills.
-  uint4 sv[NSTG];
-  int sd[NSTG];
+  U4s<2 * StageMap<D, HE, T>::NS> sv;
   if constexpr (MORE) {
-#pragma unroll
-    for (int k = 0; k < NSTG; ++k) {
-      const StageChunk<D, HE> sc = stage_chunk<D, HE>(p, k, next_pos0, qp, dist);
-      sv[k] = rope ? *sc.src : uint4{0, 0, 0, 0};
-      sd[k] = sc.dst;
-    }
+    if (rope)
+      sv = stage_fetch<D, HE, T>(p, smap, next_pos0, qp, dist);
+    else
+      sv = U4s<2 * StageMap<D, HE, T>::NS>{};
   }
-  half4_t lg[ONE ? 1 : TPW];  // ONE = false: four logits per tile
-  float lg1[ONE ? TPW : 1];   // ONE = true: one logit per tile
 #pragma unroll
   for (int i = 0; i < TPW; ++i) {
     const int gr = i / 4, ii = i % 4;
@@ -464,9 +528,10 @@ __device__ __forceinline__ void cold_range(const DecodeParams& p, CB& cb, const 
         rotate_he<D>(x1, x2, lds_rope<D, true>(rope_cur, row, g * G::NV),
                      lds_rope<D, true>(rope_cur, row, RS::HCH + g * G::NV), ya);
       } else {
+        // staged row: cos1 | cos2 | sin1 | sin2
         rotate<D>(x1, x2, lds_rope<D, false>(rope_cur, row, g * G::NV),
-                  lds_rope<D, false>(rope_cur, row, RS::HCH + g * G::NV),
                   lds_rope<D, false>(rope_cur, row, 2 * RS::HCH + g * G::NV),
+                  lds_rope<D, false>(rope_cur, row, RS::HCH + g * G::NV),
                   lds_rope<D, false>(rope_cur, row, 3 * RS::HCH + g * G::NV), dist ? kRotDist : kRotColdAbs, ya);
       }
     }
@@ -475,48 +540,63 @@ __device__ __forceinline__ void cold_range(const DecodeParams& p, CB& cb, const 
     for (int s = 0; s < G::DS; ++s) sacc = mfma_16x16x32(ya[s], qb[s], sacc);
     if constexpr (ONE) {
       const float l = (float)fp16_logit(pick4(sacc, lr) * cb.sk[i], p.scale);
-      lg1[i] = lr.valid ? l : -INFINITY;
+      lg.v[i] = lr.valid ? l : -INFINITY;
       if constexpr (MORE) cb.sk[i] = load_scale<PRM, ONE>(p, nsrc.skp, i);
     } else {
       // lane holds head n, range tokens tg + jj, tg = 64 gr + 16 g + 4 ii
       const int tg = gr * 64 + 16 * g + 4 * ii;
 #pragma unroll
-      for (int jj = 0; jj < 4; ++jj) lg[i][jj] = fp16_logit(sacc[jj] * cb.sk[i][jj], p.scale);
+      for (int jj = 0; jj < 4; ++jj) lg.v[i][jj] = fp16_logit(sacc[jj] * cb.sk[i][jj], p.scale);
       if constexpr (MORE) cb.sk[i] = load_scale<PRM, ONE>(p, nsrc.skp, i);
       if constexpr (GEN) {
         uint32_t keep = 0xffffffffu;
         if (mrow) keep = *reinterpret_cast<const uint32_t*>(mrow + tg);
 #pragma unroll
         for (int jj = 0; jj < 4; ++jj) {
-          if (lrow) lrow[tg + jj] = (float)lg[i][jj];
-          if (!((keep >> (8 * jj)) & 0xffu)) lg[i][jj] = (h16)(-INFINITY);
+          if (lrow) lrow[tg + jj] = (float)lg.v[i][jj];
+          if (!((keep >> (8 * jj)) & 0xffu)) lg.v[i][jj] = (h16)(-INFINITY);
         }
       }
     }
   }
   if constexpr (MORE) {
-    if (stage) {
-#pragma unroll
-      for (int k = 0; k < NSTG; ++k) *reinterpret_cast<uint4*>(rope_next + sd[k]) = sv[k];
-    }
+    if (stage) stage_store<D, HE, T>(rope_next, smap, sv);
   }
-  // ---- B. range maximum, merged into the running maximum
+}
+
+// Phase B: the range maximum merged into the running maximum.  Returns the
+// subtrahend of the range's exponents (msub) and the rescale of the
+// accumulators summed before this range (alpha; applied to the partial sum
+// here and to P . C_V in phase C).
+template <bool ONE, int TPW, int KV>
+__device__ __forceinline__ void range_max(const RangeLogits<ONE, TPW>& lg, ColdState<KV>& st, float& msub,
+                                          float& alpha) {
   float mloc;
   if constexpr (ONE) {
-    mloc = lg1[0];
+    mloc = lg.v[0];
 #pragma unroll
-    for (int i = 1; i < TPW; ++i) mloc = fmaxf(mloc, lg1[i]);
+    for (int i = 1; i < TPW; ++i) mloc = fmaxf(mloc, lg.v[i]);
     mloc *= kLog2e;
   } else {
-    mloc = lane_max_log2<TPW>(lg);
+    mloc = lane_max_log2<TPW>(lg.v);
   }
   const float mr = head_max<ONE>(mloc);
   const float m_new = fmaxf(st.m2, mr);
-  const float msub = (m_new == -INFINITY) ? 0.f : m_new;
-  const float alpha = fast_exp2(st.m2 - msub);  // exp2(-inf) = 0 on the first range
+  msub = (m_new == -INFINITY) ? 0.f : m_new;
+  alpha = fast_exp2(st.m2 - msub);  // exp2(-inf) = 0 on the first range
   st.m2 = m_new;
   st.l *= alpha;
-  // ---- C. probabilities and P . C_V
+}
+
+// Phase C: probabilities and P . C_V with the V codes and scales in cb.  With
+// MORE each V register is refilled from vsrc right after its last use.
+template <int KV, int TPW, bool GEN, int PRM, bool MORE, class CB>
+__device__ __forceinline__ void range_values(const DecodeParams& p, CB& cb, const CodeSrc vsrc,
+                                             const RangeLogits<!GEN, TPW>& lg, float msub, float alpha, float vn,
+                                             ColdState<KV>& st) {
+  constexpr bool ONE = !GEN;
+  const int n = threadIdx.x & 15;
+  const Lanes lr = lane_roles<ONE>(n, p.nrep);
 #pragma unroll
   for (int nt = 0; nt < CB::NT; ++nt) st.pacc[nt] *= alpha;
 #pragma unroll
@@ -524,20 +604,20 @@ __device__ __forceinline__ void cold_range(const DecodeParams& p, CB& cb, const 
     const int gr = i / 4, ii = i % 4;
     half4_t pb;
     if constexpr (ONE) {
-      const float pv = fast_exp2(__builtin_fmaf(lg1[i], kLog2e, -msub));
+      const float pv = fast_exp2(__builtin_fmaf(lg.v[i], kLog2e, -msub));
       st.l += pv;
       pb = quad_gather_h4(pv * cb.sv[i] * vn, lr.psel);
     } else {
       float pv[4];
 #pragma unroll
       for (int jj = 0; jj < 4; ++jj) {
-        pv[jj] = fast_exp2(__builtin_fmaf((float)lg[i][jj], kLog2e, -msub));
+        pv[jj] = fast_exp2(__builtin_fmaf((float)lg.v[i][jj], kLog2e, -msub));
         st.l += pv[jj];
       }
       const float4_t svn = cb.sv[i] * vn;
       pb = (half4_t){(h16)(pv[0] * svn[0]), (h16)(pv[1] * svn[1]), (h16)(pv[2] * svn[2]), (h16)(pv[3] * svn[3])};
     }
-    if constexpr (MORE) cb.sv[i] = load_scale<PRM, ONE>(p, nsrc.svp, i);
+    if constexpr (MORE) cb.sv[i] = load_scale<PRM, ONE>(p, vsrc.svp, i);
 #pragma unroll
     for (int nt = 0; nt < CB::NT; ++nt) {
       const uint4 w4 = cb.vc[gr][nt];
@@ -545,7 +625,7 @@ __device__ __forceinline__ void cold_range(const DecodeParams& p, CB& cb, const 
       st.pacc[nt] = mfma_16x16x16(i8x4_to_h4(word), pb, st.pacc[nt]);
     }
     if constexpr (MORE) {
-      if (ii == 3) load_vc(p, nsrc, gr, cb);
+      if (ii == 3) load_vc(p, vsrc, gr, cb);
     }
   }
 }
@@ -564,25 +644,51 @@ struct TailFetch {
   Half8s<Geo<D>::NV> kx1, kx2;
   half8_t vq[D / 32];
   int kpos;
+  Half8s<Geo<D>::NV> c1, s1, c2, s2;  // RoPE entries at kpos (tail_fetch_rope); c2/s2 when the halves differ
 };
 
+// ok = false (no tail tile for this unit) still issues the loads, from the
+// first D elements of Q and the sequence's counters, so that callers can
+// prefetch without a branch: a branch around loads leaves the wait counts
+// after it conservative, and later waits would also cover unrelated loads.
 template <int D>
-__device__ __forceinline__ void tail_fetch(const DecodeParams& p, int b, int h, int t0, int tl, int th,
+__device__ __forceinline__ void tail_fetch(const DecodeParams& p, int b, int h, int t0, int tl, int th, bool ok,
                                            TailFetch<D>& f) {
   using G = Geo<D>;
   const int lane = threadIdx.x & 63, g = lane >> 4, n = lane & 15;
   const long bh = (long)(b * p.Hkv + h);
+  const int cap = p.TCAP > 0 ? p.TCAP : 1;
   const int t = t0 + n;
-  const int slot = (th + (t < tl ? t : 0)) % p.TCAP;
-  f.kpos = p.tail_pos[(long)b * p.TCAP + slot];
-  const h16* krow = p.tail_k + (bh * p.TCAP + slot) * D + g * G::QG;
+  const int slot = ok ? (th + (t < tl ? t : 0)) % cap : 0;
+  const int32_t* pos = ok ? p.tail_pos + (long)b * p.TCAP : p.counters;
+  const h16* kb = ok ? p.tail_k + bh * p.TCAP * D : p.q;
+  const h16* vb = ok ? p.tail_v + bh * p.TCAP * D : p.q;
+  f.kpos = pos[slot];
+  const h16* krow = kb + (long)slot * D + g * G::QG;
   f.kx1 = load_h8s<G::NV>(krow);
   f.kx2 = load_h8s<G::NV>(krow + G::HALF);
   const int t2 = t0 + (lane >> 2);
-  const int vslot = (th + (t2 < tl ? t2 : 0)) % p.TCAP;
-  const h16* vrow = p.tail_v + (bh * p.TCAP + vslot) * D + (lane & 3) * (D / 4);
+  const int vslot = ok ? (th + (t2 < tl ? t2 : 0)) % cap : 0;
+  const h16* vrow = vb + (long)vslot * D + (lane & 3) * (D / 4);
 #pragma unroll
   for (int q = 0; q < D / 32; ++q) f.vq[q] = *reinterpret_cast<const half8_t*>(vrow + 8 * q);
+}
+
+// The RoPE table entries of the key a lane rotates (position f.kpos), issued
+// once the position has arrived.
+template <int D, bool HE>
+__device__ __forceinline__ void tail_fetch_rope(const DecodeParams& p, bool rope, TailFetch<D>& f) {
+  using G = Geo<D>;
+  const int g = (threadIdx.x & 63) >> 4;
+  if (rope) {
+    const long r = (long)clamp_angle(f.kpos, p.rope_len) * p.rope_stride + g * G::QG;
+    f.c1 = load_h8s<G::NV>(p.cos + r);
+    f.s1 = load_h8s<G::NV>(p.sin + r);
+    if constexpr (!HE) {
+      f.c2 = load_h8s<G::NV>(p.cos + r + G::HALF);
+      f.s2 = load_h8s<G::NV>(p.sin + r + G::HALF);
+    }
+  }
 }
 
 // One FP16 tail tile (tokens t0 .. t0 + 15 of one KV head, loads in f),
@@ -613,13 +719,11 @@ __device__ __forceinline__ void tail_tile(const DecodeParams& p, int b, int h, i
   if (!rope) {
     unrotated<D>(f.kx1, f.kx2, ya);
   } else {
-    const long r = (long)clamp_angle(f.kpos, p.rope_len) * p.rope_stride + g * G::QG;
-    const Half8s<G::NV> c1 = load_h8s<G::NV>(p.cos + r), s1 = load_h8s<G::NV>(p.sin + r);
     if constexpr (HE) {
-      rotate_he<D>(f.kx1, f.kx2, c1, s1, ya);
+      rotate_he<D>(f.kx1, f.kx2, f.c1, f.s1, ya);
     } else {
-      const Half8s<G::NV> c2 = load_h8s<G::NV>(p.cos + r + G::HALF), s2 = load_h8s<G::NV>(p.sin + r + G::HALF);
-      rotate<D>(f.kx1, f.kx2, c1, s1, c2, s2, p.rope_mode == SC_ROPE_DISTANCE ? kRotDist : kRotTailAbs, ya);
+      rotate<D>(f.kx1, f.kx2, f.c1, f.s1, f.c2, f.s2, p.rope_mode == SC_ROPE_DISTANCE ? kRotDist : kRotTailAbs,
+                ya);
     }
   }
   // stage the V tile ([16 tokens][kVRow]); 8-byte stores, wave-private
@@ -708,7 +812,8 @@ __device__ __forceinline__ void tail_tiles(const DecodeParams& p, int b, int h, 
   tail_tile<D, GEN, HE>(p, b, h, j * kTile, tl, ncold, qb, vs, first, sm, oacc);
   for (int tt = j + p.units_per_bh; tt < ntile; tt += p.units_per_bh) {
     TailFetch<D> f;
-    tail_fetch<D>(p, b, h, tt * kTile, tl, th, f);
+    tail_fetch<D>(p, b, h, tt * kTile, tl, th, true, f);
+    tail_fetch_rope<D, HE>(p, !GEN || p.rope_mode != SC_ROPE_NONE, f);
     tail_tile<D, GEN, HE>(p, b, h, tt * kTile, tl, ncold, qb, vs, f, sm, oacc);
   }
 }
@@ -756,9 +861,12 @@ __device__ void cold_unit(const DecodeParams& p, int b, int hq, int j, char* sme
   constexpr int T = kTile * TPW;
   constexpr int NT = KV / 16;
   constexpr int KC = CB::KC;
-  const int lane = threadIdx.x & 63, w = threadIdx.x >> 6, g = lane >> 4, n = lane & 15;
+  const int lane = threadIdx.x & 63, g = lane >> 4, n = lane & 15;
+  const int w = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);  // wave-uniform: per-head bases in SGPRs
   const int h = hq * kWaves + w;
-  const bool hvalid = h < p.Hkv;
+  // The branch-free path runs only when the KV heads fill whole groups of
+  // four: with no idle wave, its loads are issued without branches.
+  const bool hvalid = !GEN || h < p.Hkv;
   const int nrep = p.nrep;
   const Lanes lr = lane_roles<ONE>(n, nrep);
   const int qhead = ONE ? n >> 2 : n;  // query head of this lane's MFMA column
@@ -783,7 +891,12 @@ __device__ void cold_unit(const DecodeParams& p, int b, int hq, int j, char* sme
     const int* cnt = p.counters + b * SC_NCOUNTERS;
     if (p.fold_tail && j * kTile < cnt[SC_CNT_TAIL_LEN]) {
       TailFetch<D> tf;
-      tail_fetch<D>(p, b, h, j * kTile, cnt[SC_CNT_TAIL_LEN], cnt[SC_CNT_TAIL_HEAD], tf);
+      tail_fetch<D>(p, b, h, j * kTile, cnt[SC_CNT_TAIL_LEN], cnt[SC_CNT_TAIL_HEAD], true, tf);
+      const bool trope = !GEN || p.rope_mode != SC_ROPE_NONE;
+      if (he)
+        tail_fetch_rope<D, true>(p, trope, tf);
+      else
+        tail_fetch_rope<D, false>(p, trope, tf);
       if (he)
         tail_tiles<D, GEN, true>(p, b, h, j, qt, smem + w * kTile * kVRow * 2, tf, sm, oacc);
       else if constexpr (GEN)
@@ -801,19 +914,10 @@ __device__ void cold_unit(const DecodeParams& p, int b, int hq, int j, char* sme
   constexpr int RBUF = T * RS::ROW;  // bytes of one staged range
 
   // ---- prologue: RoPE rows of range 0 (L2) first, then the HBM loads
-  constexpr int NSTG = T * RS::CH / kThreads;
-  if (rope) {
-    uint4 v[NSTG];
-    int dst[NSTG];
-#pragma unroll
-    for (int k = 0; k < NSTG; ++k) {
-      const StageChunk<D, HE> s = stage_chunk<D, HE>(p, k, start, qp, dist);
-      v[k] = *s.src;
-      dst[k] = s.dst;
-    }
-#pragma unroll
-    for (int k = 0; k < NSTG; ++k) *reinterpret_cast<uint4*>(smem + dst[k]) = v[k];
-  }
+  using SM = StageMap<D, HE, T>;
+  const SM smap = stage_map<D, HE, T>(p, dist);
+  U4s<2 * SM::NS> sv0{};  // range 0's RoPE rows: requested before the HBM loads, stored after them
+  if (rope) sv0 = stage_fetch<D, HE, T>(p, smap, start, qp, dist);
   CB cb0;  // codes of the current range, refilled in place with the next
   half8_t a8[G::MT][KC];
   half4_t a4[G::MT];
@@ -842,6 +946,7 @@ __device__ void cold_unit(const DecodeParams& p, int b, int hq, int j, char* sme
     }
     vn = p.vnorm[bhj];
   }
+  if (rope) stage_store<D, HE, T>(smem, smap, sv0);
   const long cache_tok = (long)j * p.TB;  // cache-order index of the block's first token
   const uint8_t* mrow = nullptr;
   float* lrow = nullptr;
@@ -856,37 +961,58 @@ __device__ void cold_unit(const DecodeParams& p, int b, int hq, int j, char* sme
   for (int nt = 0; nt < NT; ++nt) st.pacc[nt] = (float4_t)0.f;
   __syncthreads();
 
-  // ---- ranges (the last one peeled: no refill, no staging)
-  auto range = [&](auto more_tag, int rr) {
+  // ---- ranges: step rr runs phase A of range rr, phase C of range rr - 1
+  // (whose V codes are refilled with range rr's) and phase B of range rr.
+  // The last range is peeled (no K refill, no staging) and its phase C
+  // follows the loop.
+  RangeLogits<ONE, TPW> lgp;  // logits of the previous range
+  float msp = 0.f, alp = 1.f;
+  auto step = [&](auto more_tag, auto prev_tag, int rr) __attribute__((always_inline)) {
     constexpr bool M = decltype(more_tag)::value;
+    constexpr bool P = decltype(prev_tag)::value;
     char* cur = smem + (rr & 1) * RBUF;
     char* next = smem + ((rr + 1) & 1) * RBUF;
     if (hvalid) {
-      cold_range<D, KK, KV, TPW, GEN, HE, PRM, M>(p, cb0, code_src<KK, KV>(p, bhj, (rr + 1) * T), a8, a4, qb, cur,
-                                                   next, start + (rr + 1) * T, qp, dist, rope, vn,
-                                                   mrow ? mrow + rr * T : nullptr, lrow ? lrow + rr * T : nullptr, st);
+      RangeLogits<ONE, TPW> lg;
+      range_scores<D, KK, KV, TPW, GEN, HE, PRM, M>(p, cb0, code_src<KK, KV>(p, bhj, (rr + 1) * T), a8, a4, qb, smap,
+                                                     cur, next, start + (rr + 1) * T, qp, dist, rope,
+                                                     mrow ? mrow + rr * T : nullptr, lrow ? lrow + rr * T : nullptr,
+                                                     lg);
+      if constexpr (P)
+        range_values<KV, TPW, GEN, PRM, true>(p, cb0, code_src<KK, KV>(p, bhj, rr * T), lgp, msp, alp, vn, st);
+      range_max<ONE, TPW>(lg, st, msp, alp);
+      lgp = lg;
     } else if (M && rope) {
       // idle head slot: still stage its share of the next range's rows
-      uint4 v[NSTG];
-      int dst[NSTG];
-#pragma unroll
-      for (int k = 0; k < NSTG; ++k) {
-        const StageChunk<D, HE> s = stage_chunk<D, HE>(p, k, start + (rr + 1) * T, qp, dist);
-        v[k] = *s.src;
-        dst[k] = s.dst;
-      }
-#pragma unroll
-      for (int k = 0; k < NSTG; ++k) *reinterpret_cast<uint4*>(next + dst[k]) = v[k];
+      stage_store<D, HE, T>(next, smap, stage_fetch<D, HE, T>(p, smap, start + (rr + 1) * T, qp, dist));
     }
     __syncthreads();
   };
-  for (int rr = 0; rr + 1 < R; ++rr) range(std::integral_constant<bool, true>(), rr);
+  using TT = std::integral_constant<bool, true>;
+  using FF = std::integral_constant<bool, false>;
+  if (R > 1) {
+    step(TT(), FF(), 0);
+    for (int rr = 1; rr + 1 < R; ++rr) step(TT(), TT(), rr);
+  }
   // the first FP16 tail tile of this workgroup is loaded during the last range
   TailFetch<D> tf;
   const int tl = p.counters[b * SC_NCOUNTERS + SC_CNT_TAIL_LEN];
   const bool has_tail = p.fold_tail && hvalid && j * kTile < tl;
-  if (has_tail) tail_fetch<D>(p, b, h, j * kTile, tl, p.counters[b * SC_NCOUNTERS + SC_CNT_TAIL_HEAD], tf);
-  range(std::integral_constant<bool, false>(), R - 1);
+  tail_fetch<D>(p, b, h, j * kTile, tl, p.counters[b * SC_NCOUNTERS + SC_CNT_TAIL_HEAD], has_tail, tf);
+  // the V basis of the final projection is loaded during the last range too
+  half4_t bvf[G::MT][NT];
+  const h16* bvb = p.basis_v + bhj * (long)D * KV;
+#pragma unroll
+  for (int mt = 0; mt < G::MT; ++mt)
+#pragma unroll
+    for (int nt = 0; nt < NT; ++nt)
+      bvf[mt][nt] = *reinterpret_cast<const half4_t*>(bvb + (long)(16 * mt + n) * KV + 16 * nt + 4 * g);
+  if (R > 1)
+    step(FF(), TT(), R - 1);
+  else
+    step(FF(), FF(), 0);
+  tail_fetch_rope<D, HE>(p, rope, tf);  // positions arrived during the last range (unconditional: no branch)
+  if (hvalid) range_values<KV, TPW, GEN, PRM, false>(p, cb0, CodeSrc{}, lgp, msp, alp, vn, st);
   if (!hvalid) return;
   // ---- FP16 tail tiles of this workgroup, merged into the running state
   float4_t oacc[G::MT];
@@ -907,13 +1033,6 @@ __device__ void cold_unit(const DecodeParams& p, int b, int hq, int j, char* sme
   // ---- projection O^T[d][column] = B_V^T[d][i] . Pacc[i][column] on MFMA;
   // Pacc (coefficient i = 16 nt + 4 g + jj of column n, already the
   // B-operand layout) is split into fp16 hi + lo parts to keep fp32 accuracy.
-  half4_t bvf[G::MT][NT];
-  const h16* bvb = p.basis_v + bhj * (long)D * KV;
-#pragma unroll
-  for (int mt = 0; mt < G::MT; ++mt)
-#pragma unroll
-    for (int nt = 0; nt < NT; ++nt)
-      bvf[mt][nt] = *reinterpret_cast<const half4_t*>(bvb + (long)(16 * mt + n) * KV + 16 * nt + 4 * g);
   half4_t ph[NT], pl[NT];
 #pragma unroll
   for (int nt = 0; nt < NT; ++nt)
@@ -1203,9 +1322,9 @@ extern "C" int sc_decode_attn(const ScDecodeArgs* args, void* workspace, size_t 
   hipStream_t s = (hipStream_t)stream;
   const int kk = args->tier->kp_keys, kv = args->tier->kp_values;
   // The branch-free path keeps one logit per lane, which needs GQA groups
-  // of at most 4 query heads.
+  // of at most 4 query heads, and has no idle waves (KV heads a multiple of 4).
   const bool gen = args->mask || args->logits_out || args->rope_mode == SC_ROPE_NONE || !args->halves_equal ||
-                   args->q_heads / args->tier->kv_heads > 4;
+                   args->q_heads / args->tier->kv_heads > 4 || args->tier->kv_heads % kWaves != 0;
   if (D == 128)
     return gen ? dispatch_kk<128, true>(p, kk, kv, s) : dispatch_kk<128, false>(p, kk, kv, s);
   return gen ? dispatch_kk<64, true>(p, kk, kv, s) : dispatch_kk<64, false>(p, kk, kv, s);
