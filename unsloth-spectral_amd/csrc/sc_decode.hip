@@ -498,14 +498,20 @@ __device__ __forceinline__ void range_scores(const DecodeParams& p, CB& cb, cons
     float4_t x[G::MT];
     if constexpr (KK == 16) {
       const half4_t bc = i8x4_to_h4(cb.kc[i][0]);
-      if constexpr (MORE) load_kc<KK>(nsrc, i, cb);
+      if constexpr (MORE) {
+        load_kc<KK>(nsrc, i, cb);
+        pin_vmem();
+      }
 #pragma unroll
       for (int mt = 0; mt < G::MT; ++mt) x[mt] = mfma_16x16x16(a4[mt], bc, (float4_t)0.f);
     } else {
       half8_t bc[CB::KC];
 #pragma unroll
       for (int c = 0; c < CB::KC; ++c) bc[c] = i8x8_to_h8(cb.kc[i][c]);
-      if constexpr (MORE) load_kc<KK>(nsrc, i, cb);
+      if constexpr (MORE) {
+        load_kc<KK>(nsrc, i, cb);
+        pin_vmem();
+      }
 #pragma unroll
       for (int mt = 0; mt < G::MT; ++mt) {
         float4_t acc = (float4_t)0.f;
@@ -625,7 +631,10 @@ __device__ __forceinline__ void range_values(const DecodeParams& p, CB& cb, cons
       st.pacc[nt] = mfma_16x16x16(i8x4_to_h4(word), pb, st.pacc[nt]);
     }
     if constexpr (MORE) {
-      if (ii == 3) load_vc(p, vsrc, gr, cb);
+      if (ii == 3) {
+        load_vc(p, vsrc, gr, cb);
+        pin_vmem();
+      }
     }
   }
 }
