@@ -45,7 +45,7 @@ constexpr int kThreads = 64 * kWaves;
 constexpr int kTile = 16;
 constexpr int kMaxRep = 16;
 constexpr int kVRow = 132;                              // LDS row (halves) of a staged V tile
-constexpr int kCombineWaves = 16;
+constexpr int kCombineWaves = 4;  // waves (query heads) per combine workgroup
 constexpr float kLog2e = 1.4426950408889634f;
 
 struct DecodeParams {
@@ -1093,65 +1093,49 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(2))) v
 }
 
 // Log-sum-exp merge of the partial records of one (sequence, query head):
-// wave w folds the records u = w (mod 16), then the waves merge in LDS.
+// one wave per query head, lane l owns d = E l .. E l + E - 1.  The records
+// of U units are loaded together (m and l are wave-uniform broadcasts), then
+// folded in registers.
 template <int D>
 __global__ __launch_bounds__(64 * kCombineWaves) void decode_combine_kernel(DecodeParams p) {
   constexpr int PREC = Geo<D>::PREC;
   constexpr int E = D / 64;  // d values per lane
-  constexpr int U = 8;       // records in flight per wave
-  __shared__ float s_m[kCombineWaves], s_l[kCombineWaves], s_o[kCombineWaves][D];
-  const int bq = blockIdx.x;
-  const int b = bq / p.Hq, qh = bq % p.Hq;
+  constexpr int U = 16;      // records in flight per wave
+  const int wq = blockIdx.x * kCombineWaves + (threadIdx.x >> 6);
+  if (wq >= p.B * p.Hq) return;
+  const int b = wq / p.Hq, qh = wq % p.Hq;
   const int h = qh / p.nrep, hh = qh % p.nrep;
-  const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
+  const int lane = threadIdx.x & 63;
+  const int W = p.units_per_bh;
+  const float* r0 = record_ptr(p, b, h, 0, hh, PREC);
+  const long us = (long)p.nrep * PREC;
   float M = -INFINITY, L = 0.f, O[E];
 #pragma unroll
   for (int e = 0; e < E; ++e) O[e] = 0.f;
-  for (int u0 = w; u0 < p.units_per_bh; u0 += U * kCombineWaves) {
+  for (int u0 = 0; u0 < W; u0 += U) {
     float mr[U], lr[U], orr[U][E];
 #pragma unroll
     for (int k = 0; k < U; ++k) {
-      const int u = u0 + k * kCombineWaves;
-      const float* r = record_ptr(p, b, h, u < p.units_per_bh ? u : 0, hh, PREC);
-      const bool ok = u < p.units_per_bh;
-      mr[k] = ok ? r[0] : -INFINITY;
-      lr[k] = ok ? r[1] : 0.f;
+      const float* r = r0 + (long)min(u0 + k, W - 1) * us;
+      mr[k] = u0 + k < W ? r[0] : -INFINITY;
+      lr[k] = r[1];
 #pragma unroll
-      for (int e = 0; e < E; ++e) orr[k][e] = ok ? r[4 + lane + 64 * e] : 0.f;
+      for (int e = 0; e < E; ++e) orr[k][e] = r[4 + E * lane + e];
     }
 #pragma unroll
     for (int k = 0; k < U; ++k) {
       if (mr[k] == -INFINITY) continue;
-      const float Mn = fmaxf(M, mr[k]);
-      const float a = (M == -INFINITY) ? 0.f : fast_exp2(M - Mn);
-      const float bb = fast_exp2(mr[k] - Mn);
-      L = L * a + lr[k] * bb;
+      const float mn = fmaxf(M, mr[k]);
+      const float a = fast_exp2(M - mn), c = fast_exp2(mr[k] - mn);
+      L = L * a + lr[k] * c;
 #pragma unroll
-      for (int e = 0; e < E; ++e) O[e] = O[e] * a + orr[k][e] * bb;
-      M = Mn;
+      for (int e = 0; e < E; ++e) O[e] = O[e] * a + orr[k][e] * c;
+      M = mn;
     }
   }
-  if (lane == 0) {
-    s_m[w] = M;
-    s_l[w] = L;
-  }
+  h16* o = p.out + b * p.out_sb + (long)qh * p.out_sh + E * lane;
 #pragma unroll
-  for (int e = 0; e < E; ++e) s_o[w][lane + 64 * e] = O[e];
-  __syncthreads();
-  for (int d = threadIdx.x; d < D; d += 64 * kCombineWaves) {
-    float Mt = -INFINITY;
-#pragma unroll
-    for (int ww = 0; ww < kCombineWaves; ++ww) Mt = fmaxf(Mt, s_m[ww]);
-    float Lt = 0.f, Ot = 0.f;
-#pragma unroll
-    for (int ww = 0; ww < kCombineWaves; ++ww) {
-      if (s_m[ww] == -INFINITY) continue;
-      const float a = fast_exp2(s_m[ww] - Mt);
-      Lt += a * s_l[ww];
-      Ot += a * s_o[ww][d];
-    }
-    p.out[b * p.out_sb + (long)qh * p.out_sh + d] = (h16)(Ot / Lt);
-  }
+  for (int e = 0; e < E; ++e) o[e] = (h16)(O[e] / L);
 }
 
 bool padded_rank_ok(int kp) { return kp == 16 || kp == 32 || kp == 64; }
@@ -1280,7 +1264,8 @@ int launch(DecodeParams& p, hipStream_t s) {
     int rc = sc_launch_status("decode_partial_kernel");
     if (rc) return rc;
   }
-  hipLaunchKernelGGL((decode_combine_kernel<D>), dim3(p.B * p.Hq), dim3(64 * kCombineWaves), 0, s, p);
+  const int cgrid = (p.B * p.Hq + kCombineWaves - 1) / kCombineWaves;
+  hipLaunchKernelGGL((decode_combine_kernel<D>), dim3(cgrid), dim3(64 * kCombineWaves), 0, s, p);
   return sc_launch_status("decode_combine_kernel");
 }
 
