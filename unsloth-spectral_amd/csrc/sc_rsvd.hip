@@ -3,7 +3,7 @@
 // Replaces batched_randomized_svd (rsvd.py:74-157) and the quantising part
 // of _compress_tensor (spectral_cache.py:321-407, 481-516).
 //
-// Per matrix M [rows <= 512][cols in {64,128}] (fp16, exact in fp32):
+// Per matrix M [rows <= 512][cols in {64,128}] (fp16/bf16/fp32, exact in fp32):
 //   Z   <- Omega                                   (given, or Philox4x32-10)
 //   Y   <- M Z ;  Y <- orth(Y)                      \  n_iter times:
 //   Z   <- M^T Y ; Y <- M Z ; Y <- orth(Y)          /  same subspace as the
@@ -12,11 +12,14 @@
 //   eig(Bp Bp^T) = W diag(lambda) W^T               (fp64 parallel Jacobi)
 //   S = sqrt(lambda), Vh_i = (Bp^T W)_i / S_i (normalised), coeffs = Q W S
 //   INT8 per head / per row, basis fp16.
-// orth() is CholeskyQR in fp64 (one pass between iterations, two passes for
-// the final Q); columns whose Cholesky pivot vanishes are zeroed, so
-// rank-deficient blocks (zeros, repeated rows) stay finite.
-// Thread t owns rows t and t+256 of Y/Q in registers; Y, Bp^T, the Gram
-// matrices and W live in LDS.
+// Y, Z, Bp^T, the Gram matrices and W live in LDS.  For fp16 input the
+// products with M run on MFMA (16x16x32 f16, the fp32 factor split into fp16
+// hi + lo parts, so the result keeps fp32 accuracy) and the Gram matrices on
+// the fp64 MFMA; other input types use fp32 VALU products.  orth() is
+// CholeskyQR (one pass between iterations, two for the final Q): fp64
+// Cholesky by one wave with its rows in registers, then a forward solve of
+// every row of Y against R.  Columns whose Cholesky pivot vanishes are
+// zeroed, so rank-deficient blocks (zeros, repeated rows) stay finite.
 #include <math.h>
 
 #include "sc_common.h"
@@ -169,7 +172,7 @@ constexpr size_t lds_bytes() {
 
 // y[c] = sum_d M[row][d] Zs[d][c]
 template <int RM>
-__device__ void gemm_rows(const Job& j, int rows, int cols, const float* Zs, float (&y0)[RM], float (&y1)[RM]) {
+__device__ __forceinline__ void gemm_rows(const Job& j, int rows, int cols, const float* Zs, float (&y0)[RM], float (&y1)[RM]) {
   const int t = threadIdx.x;
 #pragma unroll
   for (int c = 0; c < RM; ++c) y0[c] = y1[c] = 0.f;
@@ -201,7 +204,7 @@ __device__ void gemm_rows(const Job& j, int rows, int cols, const float* Zs, flo
 }
 
 template <int RM>
-__device__ void store_rows(float* Ys, int rows, const float (&y0)[RM], const float (&y1)[RM]) {
+__device__ __forceinline__ void store_rows(float* Ys, int rows, const float (&y0)[RM], const float (&y1)[RM]) {
   const int t = threadIdx.x;
   if (t < rows)
 #pragma unroll
@@ -213,7 +216,7 @@ __device__ void store_rows(float* Ys, int rows, const float (&y0)[RM], const flo
 
 // Zs[d][c] = sum_row M[row][d] Ys[row][c]   (M^T Y)
 template <int RM>
-__device__ void gemm_cols(const Job& j, int rows, int cols, const float* Ys, float* Zs) {
+__device__ __forceinline__ void gemm_cols(const Job& j, int rows, int cols, const float* Ys, float* Zs) {
   const int t = threadIdx.x;
   const int groups = kThreads / cols;  // 2 (cols 128) or 4 (cols 64)
   const int d = t % cols, cg = t / cols;
@@ -235,190 +238,330 @@ __device__ void gemm_cols(const Job& j, int rows, int cols, const float* Ys, flo
     if (c < cw) Zs[d * RM + c0 + c] = z[c];
 }
 
-// Gs = A^T A (fp64) for A = S[nrows][RM] (first r columns).
+// ------------------------------------------------ MFMA paths (fp16 input)
+// Products with the fp16 matrix M run on MFMA with M exact and the fp32
+// factor split into fp16 hi + lo parts (two MFMAs, fp32 accumulation): the
+// result keeps fp32 accuracy.  Gram matrices use the fp64 MFMA.
+typedef double double4_t __attribute__((ext_vector_type(4)));
+
+__device__ __forceinline__ void split16(float v, h16& hi, h16& lo) {
+  hi = (h16)v;
+  lo = (h16)(v - (float)hi);
+}
+
+// Ys[rows][RM] = M[rows][cols] Zs[cols][RM]; wave w takes row tiles w, w+4, ...
 template <int RM>
-__device__ void gram(const float* S, int nrows, int r, double* Gs) {
-  const int npairs = r * (r + 1) / 2;
-  for (int pidx = threadIdx.x; pidx < npairs; pidx += kThreads) {
-    int c1 = 0, rem = pidx;
-    while (rem >= r - c1) {
-      rem -= r - c1;
-      ++c1;
+__device__ __forceinline__ void gemm_rows_mfma(const Job& j, int rows, int cols, const float* Zs, float* Ys) {
+  constexpr int CT = (RM + 15) / 16;
+  const int lane = threadIdx.x & 63, g = lane >> 4, n = lane & 15, w = threadIdx.x >> 6;
+  const int KS = cols / 32;
+  half8_t bh[4][CT], bl[4][CT];
+#pragma unroll
+  for (int s = 0; s < 4; ++s)
+#pragma unroll
+    for (int ct = 0; ct < CT; ++ct) {
+      const int c = 16 * ct + n;
+#pragma unroll
+      for (int e = 0; e < 8; ++e) {
+        const float v = (s < KS && c < RM) ? Zs[(32 * s + 8 * g + e) * RM + c] : 0.f;
+        h16 hi, lo;
+        split16(v, hi, lo);
+        bh[s][ct][e] = hi;
+        bl[s][ct][e] = lo;
+      }
     }
-    const int c2 = c1 + rem;
-    double acc = 0.0;
-    for (int row = 0; row < nrows; ++row) acc = fma((double)S[row * RM + c1], (double)S[row * RM + c2], acc);
-    Gs[c1 * RM + c2] = acc;
-    Gs[c2 * RM + c1] = acc;
+  for (int rt = w; rt < rows / 16; rt += kThreads / 64) {
+    const h16* rp = reinterpret_cast<const h16*>(row_ptr(j, 16 * rt + n, cols));
+    half8_t a[4];
+#pragma unroll
+    for (int s = 0; s < 4; ++s)
+      a[s] = s < KS ? *reinterpret_cast<const half8_t*>(rp + 32 * s + 8 * g) : (half8_t)(h16)0;
+#pragma unroll
+    for (int ct = 0; ct < CT; ++ct) {
+      float4_t acc = (float4_t)0.f;
+#pragma unroll
+      for (int s = 0; s < 4; ++s)
+        if (s < KS) {
+          acc = __builtin_amdgcn_mfma_f32_16x16x32_f16(a[s], bh[s][ct], acc, 0, 0, 0);
+          acc = __builtin_amdgcn_mfma_f32_16x16x32_f16(a[s], bl[s][ct], acc, 0, 0, 0);
+        }
+      const int c = 16 * ct + n;
+      if (c < RM)
+#pragma unroll
+        for (int jj = 0; jj < 4; ++jj) Ys[(16 * rt + 4 * g + jj) * RM + c] = acc[jj];
+    }
   }
 }
 
-// In-place Cholesky G = L L^T (lower part of Gs), then Ws = L^{-T} (upper
-// triangular R^{-1} with R = L^T).  Vanishing pivots mark dead columns.
+// Zs[cols][RM] = M^T Ys; wave w owns d tiles w*DT .. w*DT+DT-1 (cols/16/4
+// each).  The M^T operand is gathered with 2-byte loads (8 rows of one
+// column per lane), prefetched one K step ahead.
 template <int RM>
-__device__ void cholesky_rinv(double* Gs, double* Ws, int* dead, double* red, int r) {
-  const int t = threadIdx.x;
-  if (t == 0) {
-    double gmax = 0.0;
-    for (int c = 0; c < r; ++c) gmax = fmax(gmax, Gs[c * RM + c]);
-    red[0] = gmax;
+__device__ __forceinline__ void gemm_cols_mfma(const Job& j, int rows, int cols, const float* Ys, float* Zs) {
+  constexpr int CT = (RM + 15) / 16;
+  const int lane = threadIdx.x & 63, g = lane >> 4, n = lane & 15, w = threadIdx.x >> 6;
+  const int DT = cols / 64;  // d tiles per wave: 2 (cols 128) or 1 (cols 64)
+  float4_t acc[2][CT];
+#pragma unroll
+  for (int dt = 0; dt < 2; ++dt)
+#pragma unroll
+    for (int ct = 0; ct < CT; ++ct) acc[dt][ct] = (float4_t)0.f;
+  auto gather = [&](int k0, half8_t (&a)[2]) __attribute__((always_inline)) {
+#pragma unroll
+    for (int e = 0; e < 8; ++e) {
+      const h16* rp = reinterpret_cast<const h16*>(row_ptr(j, k0 + 8 * g + e, cols));
+#pragma unroll
+      for (int dt = 0; dt < 2; ++dt) a[dt][e] = dt < DT ? rp[(w * DT + dt) * 16 + n] : (h16)0;
+    }
+  };
+  half8_t a[2], an[2];
+  gather(0, a);
+  for (int k0 = 0; k0 < rows; k0 += 32) {
+    if (k0 + 32 < rows) gather(k0 + 32, an);
+#pragma unroll
+    for (int ct = 0; ct < CT; ++ct) {
+      const int c = 16 * ct + n;
+      half8_t bh, bl;
+#pragma unroll
+      for (int e = 0; e < 8; ++e) {
+        const float v = c < RM ? Ys[(k0 + 8 * g + e) * RM + c] : 0.f;
+        h16 hi, lo;
+        split16(v, hi, lo);
+        bh[e] = hi;
+        bl[e] = lo;
+      }
+#pragma unroll
+      for (int dt = 0; dt < 2; ++dt)
+        if (dt < DT) {
+          acc[dt][ct] = __builtin_amdgcn_mfma_f32_16x16x32_f16(a[dt], bh, acc[dt][ct], 0, 0, 0);
+          acc[dt][ct] = __builtin_amdgcn_mfma_f32_16x16x32_f16(a[dt], bl, acc[dt][ct], 0, 0, 0);
+        }
+    }
+    a[0] = an[0];
+    a[1] = an[1];
+  }
+#pragma unroll
+  for (int dt = 0; dt < 2; ++dt)
+    if (dt < DT)
+#pragma unroll
+      for (int ct = 0; ct < CT; ++ct) {
+        const int c = 16 * ct + n;
+        if (c < RM)
+#pragma unroll
+          for (int jj = 0; jj < 4; ++jj) Zs[((w * DT + dt) * 16 + 4 * g + jj) * RM + c] = acc[dt][ct][jj];
+      }
+}
+
+// Gs[c1][c2] = sum_row S[row][c1] S[row][c2] (c1, c2 < r) in fp64 on MFMA.
+// Tile (ta, tb), ta <= tb, of the CT x CT upper triangle goes to wave
+// (tile index) % 4; the f64 16x16x4 output holds D[4 e + g][n] in lane
+// (g, n), element e.
+template <int RM>
+__device__ __forceinline__ void gram_mfma(const float* S, int nrows, int r, double* Gs) {
+  constexpr int CT = (RM + 15) / 16;
+  const int lane = threadIdx.x & 63, g = lane >> 4, n = lane & 15, w = threadIdx.x >> 6;
+  int tix = 0;
+  for (int ta = 0; ta < CT; ++ta)
+    for (int tb = ta; tb < CT; ++tb, ++tix) {
+      if (tix % (kThreads / 64) != w) continue;
+      const int ca = 16 * ta + n, cb = 16 * tb + n;
+      double4_t acc = {0.0, 0.0, 0.0, 0.0};
+      for (int k0 = 0; k0 < nrows; k0 += 4) {
+        const double av = ca < RM ? (double)S[(k0 + g) * RM + ca] : 0.0;
+        const double bv = cb < RM ? (double)S[(k0 + g) * RM + cb] : 0.0;
+        acc = __builtin_amdgcn_mfma_f64_16x16x4f64(av, bv, acc, 0, 0, 0);
+      }
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        const int c1 = 16 * ta + 4 * e + g, c2 = 16 * tb + n;
+        if (c1 < r && c2 < r) {
+          Gs[c1 * RM + c2] = acc[e];
+          Gs[c2 * RM + c1] = acc[e];
+        }
+      }
+    }
+}
+
+// Orders the LDS writes of a wave before its later LDS reads by other lanes.
+__device__ __forceinline__ void wave_sync() {
+  __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+  __builtin_amdgcn_wave_barrier();
+  __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+}
+
+// Reciprocal to full double precision: hardware estimate + two Newton steps.
+__device__ __forceinline__ double rcp64(double x) {
+  double y = __builtin_amdgcn_rcp(x);
+  y = fma(y, fma(-x, y, 1.0), y);
+  return fma(y, fma(-x, y, 1.0), y);
+}
+__device__ __forceinline__ double rsqrt64(double x) {
+  double y = __builtin_amdgcn_rsq(x);
+  y = y * fma(-0.5 * x * y, y, 1.5);
+  return y * fma(-0.5 * x * y, y, 1.5);
+}
+
+// Cholesky G = L L^T of Gs (r x r, r <= RM) by wave 0: lane i keeps row i
+// in registers, the steps are unrolled (register indices are static) and
+// column jc is broadcast through LDS (col).  Writes R = L^T into Ws
+// (upper triangle, row-major) and 1/R[c][c] (0 for dead columns, whose
+// pivot vanished) into rdiag.
+template <int RM>
+__device__ __forceinline__ void cholesky_wave(const double* Gs, double* Ws, double* rdiag, double* col, int r) {
+  if (threadIdx.x < 64) {
+    const int lane = threadIdx.x;
+    const bool act = lane < r;
+    double row[RM];
+#pragma unroll
+    for (int k = 0; k < RM; ++k) row[k] = (act && k < r) ? Gs[lane * RM + k] : 0.0;
+    double gm = act ? row[0] : 0.0;
+#pragma unroll
+    for (int k = 1; k < RM; ++k)
+      if (k == lane) gm = row[k];
+#pragma unroll
+    for (int o = 32; o > 0; o >>= 1) gm = fmax(gm, __shfl_xor(gm, o));
+    const double tol = gm * 1e-26 + 1e-300;
+#pragma unroll
+    for (int jc = 0; jc < RM; ++jc) {
+      if (jc < r) {  // wave-uniform
+        const double piv = __shfl(row[jc], jc);
+        const bool dead = !(piv > tol);
+        const double il = dead ? 0.0 : rsqrt64(piv);
+        if (lane > jc) row[jc] *= il;  // L[lane][jc]
+        if (lane == jc) row[jc] = dead ? 0.0 : piv * il;  // L[jc][jc] = sqrt(piv)
+        col[lane] = row[jc];
+        wave_sync();
+#pragma unroll
+        for (int k = jc + 1; k < RM; ++k)
+          if (lane > jc && k <= lane) row[k] -= row[jc] * col[k];
+        if (lane == 0) rdiag[jc] = il;
+        wave_sync();
+      }
+    }
+    // R[k][lane] = L[lane][k] for k <= lane
+#pragma unroll
+    for (int k = 0; k < RM; ++k)
+      if (act && k <= lane) Ws[k * RM + lane] = row[k];
   }
   __syncthreads();
-  const double tol = red[0] * 1e-26 + 1e-300;
-  for (int jc = 0; jc < r; ++jc) {
-    // column jc of L: pivot then scale
-    const double piv = Gs[jc * RM + jc];
-    const bool is_dead = !(piv > tol);
-    const double lj = is_dead ? 1.0 : sqrt(piv);
-    __syncthreads();
-    for (int i = jc + 1 + t; i < r; i += kThreads) Gs[i * RM + jc] = is_dead ? 0.0 : Gs[i * RM + jc] / lj;
-    if (t == 0) {
-      Gs[jc * RM + jc] = lj;
-      dead[jc] = is_dead;
-    }
-    __syncthreads();
-    const int m = r - jc - 1;
-    for (int e = t; e < m * m; e += kThreads) {
-      const int i = jc + 1 + e / m, k = jc + 1 + e % m;
-      if (k <= i) Gs[i * RM + k] -= Gs[i * RM + jc] * Gs[k * RM + jc];
-    }
-    __syncthreads();
-  }
-  // R = L^T upper.  Solve R X = I column by column (thread = column).
-  if (t < r) {
-    const int c = t;
-    for (int i = r - 1; i >= 0; --i) {
-      double v = (i == c) ? 1.0 : 0.0;
-      for (int m2 = i + 1; m2 <= c; ++m2) v -= Gs[m2 * RM + i] * Ws[m2 * RM + c];  // R[i][m2] = L[m2][i]
-      Ws[i * RM + c] = (i > c) ? 0.0 : v / Gs[i * RM + i];
-    }
-    if (dead[c])
-      for (int i = 0; i < r; ++i) Ws[i * RM + c] = 0.0;
-  }
-  __syncthreads();
 }
 
-// y <- y R^{-1}
+// Rows of Ys <- rows R^{-1} by forward substitution (q R = y, R upper
+// triangular in Ws, reciprocal diagonal in rdiag; dead columns give 0), in
+// fp64, one row at a time per thread.
 template <int RM>
-__device__ void apply_rinv(const double* Ws, int r, float (&y0)[RM], float (&y1)[RM]) {
-  float q0[RM], q1[RM];
+__device__ __forceinline__ void solve_rows(float* Ys, int rows, const double* Ws, const double* rdiag, int r) {
+  for (int row = threadIdx.x; row < rows; row += kThreads) {
+    double q[RM];
 #pragma unroll
-  for (int c = 0; c < RM; ++c) {
-    double a0 = 0.0, a1 = 0.0;
+    for (int c = 0; c < RM; ++c) {
+      double a = Ys[row * RM + c];
 #pragma unroll
-    for (int i = 0; i <= c; ++i) {
-      const double w = Ws[i * RM + c];
-      a0 = fma((double)y0[i], w, a0);
-      a1 = fma((double)y1[i], w, a1);
+      for (int i = 0; i < c; ++i) a = fma(-q[i], Ws[i * RM + c], a);
+      q[c] = c < r ? a * rdiag[c] : 0.0;
     }
-    q0[c] = c < r ? (float)a0 : 0.f;
-    q1[c] = c < r ? (float)a1 : 0.f;
-  }
 #pragma unroll
-  for (int c = 0; c < RM; ++c) {
-    y0[c] = q0[c];
-    y1[c] = q1[c];
+    for (int c = 0; c < RM; ++c) Ys[row * RM + c] = (float)q[c];
   }
 }
 
+// Cyclic parallel Jacobi on the symmetric Gs by wave 0: Gs -> diagonal,
+// Ws = eigenvectors.  The round-robin pairing runs over RM players (RM
+// even); rows and columns >= r are zeroed first, so their rotations are the
+// identity.  Loop shapes are compile-time (RM) so index arithmetic is
+// cheap; rotation parameters use the hardware reciprocal / rsqrt refined by
+// Newton steps; rows, then columns, are updated lane-parallel.
 template <int RM>
-__device__ void orth(Lds<RM>& L, int rows, int r, int passes, float (&y0)[RM], float (&y1)[RM]) {
-  for (int ps = 0; ps < passes; ++ps) {
-    __syncthreads();
-    store_rows<RM>(L.Ys, rows, y0, y1);
-    __syncthreads();
-    gram<RM>(L.Ys, rows, r, L.Gs);
-    __syncthreads();
-    cholesky_rinv<RM>(L.Gs, L.Ws, L.flag, L.red, r);
-    apply_rinv<RM>(L.Ws, r, y0, y1);
-  }
-}
-
-// Cyclic parallel Jacobi on the symmetric Gs (r x r): Gs -> diag, Ws = V.
-template <int RM>
-__device__ void jacobi_eig(double* Gs, double* Ws, double* red, int* flag, int r) {
-  const int t = threadIdx.x;
-  for (int e = t; e < RM * RM; e += kThreads) Ws[e] = (e / RM == e % RM) ? 1.0 : 0.0;
-  const int ne = r + (r & 1);  // even player count (player r is a bye when r odd)
-  double* rot = red;           // [c, s, p, q] per pair, up to 20 pairs (80 doubles)
-  __syncthreads();
-  for (int sweep = 0; sweep < 30; ++sweep) {
-    // convergence test: off-diagonal vs diagonal mass
-    if (t == 0) {
+__device__ __forceinline__ void jacobi_eig_wave(double* Gs, double* Ws, double* rot, int r) {
+  static_assert(RM % 2 == 0, "even player count");
+  constexpr int NP = RM / 2;
+  if (threadIdx.x < 64) {
+    const int lane = threadIdx.x;
+    for (int e = lane; e < RM * RM; e += 64) {
+      const int i = e / RM, k = e % RM;
+      Ws[e] = (i == k) ? 1.0 : 0.0;
+      if (i >= r || k >= r) Gs[e] = 0.0;
+    }
+    int* pq = reinterpret_cast<int*>(rot + 2 * NP);
+    wave_sync();
+    for (int sweep = 0; sweep < 30; ++sweep) {
       double off = 0.0, dia = 0.0;
-      for (int i = 0; i < r; ++i)
-        for (int k = 0; k < r; ++k) {
-          const double v = Gs[i * RM + k];
-          if (i == k)
-            dia += v * v;
-          else
-            off += v * v;
-        }
-      flag[RM] = (off <= 1e-30 * dia) || (dia == 0.0);
-    }
-    __syncthreads();
-    if (flag[RM]) break;
-    for (int step = 0; step < ne - 1; ++step) {
-      // round-robin pairing: player 0 fixed, others rotate
-      if (t < ne / 2) {
-        auto player = [&](int idx) { return idx == 0 ? 0 : 1 + (idx - 1 + step) % (ne - 1); };
-        int p = player(t), q = player(ne - 1 - t);
-        if (p > q) {
-          const int tmp = p;
-          p = q;
-          q = tmp;
-        }
-        double c = 1.0, s = 0.0;
-        if (q < r) {
-          const double apq = Gs[p * RM + q];
+      for (int e = lane; e < RM * RM; e += 64) {
+        const double v = Gs[e];
+        if (e / RM == e % RM)
+          dia += v * v;
+        else
+          off += v * v;
+      }
+#pragma unroll
+      for (int o = 32; o > 0; o >>= 1) {
+        off += __shfl_xor(off, o);
+        dia += __shfl_xor(dia, o);
+      }
+      if (off <= 1e-24 * dia || dia == 0.0) break;  // off-diagonal below 1e-12 of the diagonal
+      for (int step = 0; step < RM - 1; ++step) {
+        if (lane < NP) {
+          const int i1 = lane, i2 = RM - 1 - lane;
+          int pp = i1 == 0 ? 0 : 1 + (i1 - 1 + step) % (RM - 1);
+          int qq = 1 + (i2 - 1 + step) % (RM - 1);
+          if (pp > qq) {
+            const int tmp = pp;
+            pp = qq;
+            qq = tmp;
+          }
+          const double apq = Gs[pp * RM + qq], app = Gs[pp * RM + pp], aqq = Gs[qq * RM + qq];
+          double c = 1.0, sn = 0.0;
           if (apq != 0.0) {
-            const double app = Gs[p * RM + p], aqq = Gs[q * RM + q];
-            const double tau = (aqq - app) / (2.0 * apq);
-            const double tt = (tau >= 0.0 ? 1.0 : -1.0) / (fabs(tau) + sqrt(1.0 + tau * tau));
-            c = 1.0 / sqrt(1.0 + tt * tt);
-            s = tt * c;
+            const double tau = (aqq - app) * rcp64(2.0 * apq);
+            const double tt = (tau >= 0.0 ? 1.0 : -1.0) * rcp64(fabs(tau) + sqrt(1.0 + tau * tau));
+            c = rsqrt64(1.0 + tt * tt);
+            sn = tt * c;
+          }
+          rot[2 * lane] = c;
+          rot[2 * lane + 1] = sn;
+          pq[2 * lane] = pp;
+          pq[2 * lane + 1] = qq;
+        }
+        wave_sync();
+        // rows: A <- J^T A ; element (pair pi, column k)
+#pragma unroll
+        for (int e0 = 0; e0 < NP * RM; e0 += 64) {
+          const int e = e0 + lane;
+          if (e < NP * RM) {
+            const int pi = e / RM, k = e % RM;
+            const double c = rot[2 * pi], sn = rot[2 * pi + 1];
+            const int pp = pq[2 * pi], qq = pq[2 * pi + 1];
+            const double ap = Gs[pp * RM + k], aq = Gs[qq * RM + k];
+            Gs[pp * RM + k] = c * ap - sn * aq;
+            Gs[qq * RM + k] = sn * ap + c * aq;
           }
         }
-        rot[4 * t] = c;
-        rot[4 * t + 1] = s;
-        rot[4 * t + 2] = p;
-        rot[4 * t + 3] = q;
-      }
-      __syncthreads();
-      // rows: A <- J^T A
-      for (int e = t; e < (ne / 2) * r; e += kThreads) {
-        const int pi = e / r, k = e % r;
-        const double c = rot[4 * pi], s = rot[4 * pi + 1];
-        const int p = (int)rot[4 * pi + 2], q = (int)rot[4 * pi + 3];
-        if (q < r && s != 0.0) {
-          const double ap = Gs[p * RM + k], aq = Gs[q * RM + k];
-          Gs[p * RM + k] = c * ap - s * aq;
-          Gs[q * RM + k] = s * ap + c * aq;
+        wave_sync();
+        // columns: A <- A J, V <- V J
+#pragma unroll
+        for (int e0 = 0; e0 < NP * RM; e0 += 64) {
+          const int e = e0 + lane;
+          if (e < NP * RM) {
+            const int pi = e / RM, k = e % RM;
+            const double c = rot[2 * pi], sn = rot[2 * pi + 1];
+            const int pp = pq[2 * pi], qq = pq[2 * pi + 1];
+            const double ap = Gs[k * RM + pp], aq = Gs[k * RM + qq];
+            Gs[k * RM + pp] = c * ap - sn * aq;
+            Gs[k * RM + qq] = sn * ap + c * aq;
+            const double vp = Ws[k * RM + pp], vq = Ws[k * RM + qq];
+            Ws[k * RM + pp] = c * vp - sn * vq;
+            Ws[k * RM + qq] = sn * vp + c * vq;
+          }
         }
+        wave_sync();
       }
-      __syncthreads();
-      // columns: A <- A J, V <- V J
-      for (int e = t; e < (ne / 2) * r; e += kThreads) {
-        const int pi = e / r, k = e % r;
-        const double c = rot[4 * pi], s = rot[4 * pi + 1];
-        const int p = (int)rot[4 * pi + 2], q = (int)rot[4 * pi + 3];
-        if (q < r && s != 0.0) {
-          const double ap = Gs[k * RM + p], aq = Gs[k * RM + q];
-          Gs[k * RM + p] = c * ap - s * aq;
-          Gs[k * RM + q] = s * ap + c * aq;
-          const double vp = Ws[k * RM + p], vq = Ws[k * RM + q];
-          Ws[k * RM + p] = c * vp - s * vq;
-          Ws[k * RM + q] = s * vp + c * vq;
-        }
-      }
-      __syncthreads();
     }
   }
   __syncthreads();
 }
 
 template <int RM>
-__device__ void run_matrix(const RsvdParams& p, const Job& j, int rows, int cols, int n_iter, Lds<RM>& L,
+__device__ __forceinline__ void run_matrix(const RsvdParams& p, const Job& j, int rows, int cols, int n_iter, Lds<RM>& L,
                            const float* omega_in, long dbg_index) {
   const int t = threadIdx.x;
   const int r = j.r, k = j.k;
@@ -439,39 +582,57 @@ __device__ void run_matrix(const RsvdParams& p, const Job& j, int rows, int cols
   if (p.omega_out && dbg_index >= 0)
     for (int e = t; e < cols * r; e += kThreads) p.omega_out[dbg_index * cols * r + e] = L.Zs[(e / r) * RM + e % r];
 
-  float y0[RM], y1[RM];
-  gemm_rows<RM>(j, rows, cols, L.Zs, y0, y1);
-  orth<RM>(L, rows, r, 1, y0, y1);
+  const bool mf = j.dtype == SC_DTYPE_F16;  // MFMA products (fp16 input); else fp32 VALU
+  auto mul_m = [&]() __attribute__((always_inline)) {  // Ys = M Zs
+    if (mf) {
+      gemm_rows_mfma<RM>(j, rows, cols, L.Zs, L.Ys);
+    } else {
+      float y0[RM], y1[RM];
+      gemm_rows<RM>(j, rows, cols, L.Zs, y0, y1);
+      store_rows<RM>(L.Ys, rows, y0, y1);
+    }
+  };
+  auto mul_mt = [&]() __attribute__((always_inline)) {  // Zs = M^T Ys
+    if (mf)
+      gemm_cols_mfma<RM>(j, rows, cols, L.Ys, L.Zs);
+    else
+      gemm_cols<RM>(j, rows, cols, L.Ys, L.Zs);
+  };
+  auto orth_ys = [&](int passes) __attribute__((always_inline)) {  // Ys <- Q of Ys (CholeskyQR passes)
+    for (int ps = 0; ps < passes; ++ps) {
+      __syncthreads();
+      gram_mfma<RM>(L.Ys, rows, r, L.Gs);
+      __syncthreads();
+      cholesky_wave<RM>(L.Gs, L.Ws, L.red, L.red + RM, r);
+      solve_rows<RM>(L.Ys, rows, L.Ws, L.red, r);
+    }
+  };
+  mul_m();
+  orth_ys(1);
   for (int it = 0; it < n_iter; ++it) {
     __syncthreads();
-    store_rows<RM>(L.Ys, rows, y0, y1);
+    mul_mt();
     __syncthreads();
-    gemm_cols<RM>(j, rows, cols, L.Ys, L.Zs);
-    __syncthreads();
-    gemm_rows<RM>(j, rows, cols, L.Zs, y0, y1);
-    orth<RM>(L, rows, r, it + 1 == n_iter ? 2 : 1, y0, y1);
+    mul_m();
+    orth_ys(it + 1 == n_iter ? 2 : 1);
   }
-  if (n_iter == 0) orth<RM>(L, rows, r, 1, y0, y1);  // second pass for the final Q
+  if (n_iter == 0) orth_ys(1);  // second pass for the final Q
   // ---- Bp^T = M^T Q
   __syncthreads();
-  store_rows<RM>(L.Ys, rows, y0, y1);
+  mul_mt();
   __syncthreads();
-  gemm_cols<RM>(j, rows, cols, L.Ys, L.Zs);
+  gram_mfma<RM>(L.Zs, cols, r, L.Gs);  // Bp Bp^T
   __syncthreads();
-  gram<RM>(L.Zs, cols, r, L.Gs);  // Bp Bp^T
-  __syncthreads();
-  jacobi_eig<RM>(L.Gs, L.Ws, L.red, L.flag, r);
-  // ---- sort eigenvalues (descending)
-  if (t == 0) {
-    for (int c = 0; c < r; ++c) L.ord[c] = c;
-    for (int a = 0; a < r; ++a) {
-      int best = a;
-      for (int b2 = a + 1; b2 < r; ++b2)
-        if (L.Gs[L.ord[b2] * RM + L.ord[b2]] > L.Gs[L.ord[best] * RM + L.ord[best]]) best = b2;
-      const int tmp = L.ord[a];
-      L.ord[a] = L.ord[best];
-      L.ord[best] = tmp;
+  jacobi_eig_wave<RM>(L.Gs, L.Ws, L.red, r);
+  // ---- eigenvalues in descending order: lane c takes rank = #{larger, or equal with lower index}
+  if (t < r) {
+    const double lc = L.Gs[t * RM + t];
+    int rank = 0;
+    for (int b2 = 0; b2 < r; ++b2) {
+      const double lb = L.Gs[b2 * RM + b2];
+      rank += (lb > lc) || (lb == lc && b2 < t);
     }
+    L.ord[rank] = t;
   }
   __syncthreads();
   // Wf[c][i] = W[c][ord_i] * S_i  (i < k)
@@ -481,6 +642,26 @@ __device__ void run_matrix(const RsvdParams& p, const Job& j, int rows, int cols
     const double sv = sqrt(fmax(L.Gs[oi * RM + oi], 0.0));
     L.Wf[c * RM + i] = (float)(L.Ws[c * RM + oi] * sv);
   }
+  __syncthreads();
+  // ---- coefficients of my rows (Q in Ys): coeff[i] = sum_c Q[row][c] Wf[c][i]
+  const bool v0 = t < rows, v1 = t + kThreads < rows;
+  float cf0[RM], cf1[RM];
+#pragma unroll
+  for (int i = 0; i < RM; ++i) cf0[i] = cf1[i] = 0.f;
+#pragma unroll
+  for (int c = 0; c < RM; ++c) {
+    if (c < r) {
+      const float q0 = v0 ? L.Ys[t * RM + c] : 0.f, q1 = v1 ? L.Ys[(t + kThreads) * RM + c] : 0.f;
+#pragma unroll
+      for (int i = 0; i < RM; ++i)
+        if (i < k) {
+          const float w = L.Wf[c * RM + i];
+          cf0[i] = fmaf(q0, w, cf0[i]);
+          cf1[i] = fmaf(q1, w, cf1[i]);
+        }
+    }
+  }
+  __syncthreads();  // Q no longer needed: Ys is reused for Vh
   // Vh (unnormalised) into Ys as [k][cols]: Vh_i[d] = sum_c W[c][ord_i] Bp^T[d][c]
   for (int e = t; e < k * cols; e += kThreads) {
     const int i = e / cols, d = e % cols;
@@ -490,16 +671,20 @@ __device__ void run_matrix(const RsvdParams& p, const Job& j, int rows, int cols
     L.Ys[i * cols + d] = (float)acc;
   }
   __syncthreads();
-  if (t < k) {  // row norms -> 1/norm (0 for vanished rows)
+  for (int i = t >> 6; i < k; i += kThreads / 64) {  // row norms -> 1/norm (0 for vanished rows), one wave per row
     double nn = 0.0;
-    for (int d = 0; d < cols; ++d) {
-      const double v = L.Ys[t * cols + d];
+    for (int d = t & 63; d < cols; d += 64) {
+      const double v = L.Ys[i * cols + d];
       nn += v * v;
     }
-    L.red[t] = nn > 0.0 ? 1.0 / sqrt(nn) : 0.0;
-    if (p.svals_out && dbg_index >= 0) {
-      const int oi = L.ord[t];
-      p.svals_out[dbg_index * k + t] = (float)sqrt(fmax(L.Gs[oi * RM + oi], 0.0));
+#pragma unroll
+    for (int o = 32; o > 0; o >>= 1) nn += __shfl_xor(nn, o);
+    if ((t & 63) == 0) {
+      L.red[i] = nn > 0.0 ? 1.0 / sqrt(nn) : 0.0;
+      if (p.svals_out && dbg_index >= 0) {
+        const int oi = L.ord[i];
+        p.svals_out[dbg_index * k + i] = (float)sqrt(fmax(L.Gs[oi * RM + oi], 0.0));
+      }
     }
   }
   __syncthreads();
@@ -513,25 +698,6 @@ __device__ void run_matrix(const RsvdParams& p, const Job& j, int rows, int cols
       j.basis[(long)i * cols + d] = (h16)v;
     if (p.vh_out && dbg_index >= 0 && i < k) p.vh_out[(dbg_index * k + i) * cols + d] = v;
   }
-  // ---- coefficients of my rows: coeff[i] = sum_c Q[row][c] Wf[c][i]
-  float cf0[RM], cf1[RM];
-#pragma unroll
-  for (int i = 0; i < RM; ++i) {
-    float a0 = 0.f, a1 = 0.f;
-    if (i < k) {
-#pragma unroll
-      for (int c = 0; c < RM; ++c) {
-        if (c < r) {
-          const float w = L.Wf[c * RM + i];
-          a0 = fmaf(y0[c], w, a0);
-          a1 = fmaf(y1[c], w, a1);
-        }
-      }
-    }
-    cf0[i] = a0;
-    cf1[i] = a1;
-  }
-  const bool v0 = t < rows, v1 = t + kThreads < rows;
   if (p.coeffs_out && dbg_index >= 0) {
     for (int i = 0; i < k; ++i) {
       if (v0) p.coeffs_out[(dbg_index * rows + t) * k + i] = cf0[i];
