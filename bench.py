@@ -235,12 +235,18 @@ def copy_probe(torch, device, mib, reps=5):
 
 
 def _pmc_means(path):
-    """Mean value per dispatch of every counter, per kernel name, from the
-    rocpd databases a rocprofv3 --pmc run wrote under path."""
+    """Mean value per dispatch of every counter, per kernel name, from what a
+    rocprofv3 --pmc run wrote under path (counter_collection CSV files, or
+    rocpd databases)."""
     import collections
+    import csv
     import glob
     import sqlite3
     agg = collections.defaultdict(lambda: collections.defaultdict(list))
+    for fn in glob.glob(os.path.join(path, "**", "*counter_collection.csv"), recursive=True):
+        with open(fn) as f:
+            for r in csv.DictReader(f):
+                agg[r["Kernel_Name"]][r["Counter_Name"]].append(float(r["Counter_Value"]))
     for db in glob.glob(os.path.join(path, "**", "*_results.db"), recursive=True):
         con = sqlite3.connect(db)
         cur = con.cursor()

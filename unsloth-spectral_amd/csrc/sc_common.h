@@ -100,9 +100,9 @@ __device__ __forceinline__ half8_t i8x8_to_h8(uint2 w) {
   return (half8_t){a.x, a.y, a.z, a.w, b.x, b.y, b.z, b.w};
 }
 
-// Keeps vector-memory instructions where the source issues them: the
-// machine scheduler may move ALU and LDS work across this point but no
-// global load or store.  Used after prefetch loads that must stay early.
+// Scheduling fence: the machine scheduler moves no instruction of any kind
+// across this point (mask 0).  Placed right after prefetch loads so that they
+// are issued where the source issues them, ahead of the compute they overlap.
 __device__ __forceinline__ void pin_vmem() { __builtin_amdgcn_sched_barrier(0); }
 
 __device__ __forceinline__ half2_t pack_h2(float a, float b) {
