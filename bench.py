@@ -1,23 +1,33 @@
-"""Benchmark: spectral decode attention (C3) + rSVD block compression (C2) on one MI355X.
+"""Benchmark: spectral decode attention + rSVD block compression on one MI355X.
 
-    python bench.py [--gpus 1] [--steps K] [--warmup W] [--no-cpu] [--rotate R]
+    python bench.py [--gpus 1] [--steps K] [--warmup W] [--no-cpu] [--rotate R] [--only-headline]
+    python bench.py --model-loop [--prompt 8192] [--decode-steps 256]
     python bench.py ... --copy-probe-mib 256          (under rocprofv3 --pmc: calibration kernel)
     python bench.py --summarize-pmc FETCH_DIR WRITE_DIR --copy-probe-mib 256
 
-Workloads (synthetic data, seeds fixed):
-  decode  batch 8, context 16384 = 31 cold 512-token blocks (INT8 codes k=32,
-          one FP32 scale per row, FP16 bases) + 512 FP16 tail tokens per
-          sequence; 32 query / 8 KV heads, head_dim 128, absolute RoPE
-          (theta 1e6).  K/V are U diag(exp(-i/8)) V^T + N(0, 0.01^2) per
-          (sequence, KV head); the cold blocks are compressed on the GPU by
-          this library's rSVD (k=32, p=5, q=2) before timing.  One step = one
-          decode-attention call for one layer.  R distinct tier sets (default
-          4, ~490 MB of tiers) are rotated so that the 256 MB MALL cannot hold
-          the working set.
+Workloads (synthetic data, seeds fixed; 32 query / 8 KV heads, head_dim 128,
+absolute RoPE theta 1e6, one FP32 INT8 scale per row, 512-token blocks):
+  decode (headline)  batch 8, context 16384 = 31 cold blocks (INT8 codes k=32,
+          FP16 bases) + 512 FP16 tail tokens per sequence.  K/V are
+          U diag(exp(-i/8)) V^T + N(0, 0.01^2) per (sequence, KV head); the
+          cold blocks are compressed on the GPU by this library's rSVD (k=32,
+          p=5, q=2) before timing.  One step = one decode-attention call for
+          one layer.  R distinct tier sets (default 4, ~490 MB of tiers) are
+          rotated so that the 256 MB MALL cannot hold the working set.
+  decode, batch 1    context 4096 = 7 cold blocks k=16 + 512 tail (latency bound).
+  decode, batch 16   context 33280 = 64 cold blocks k=32 + 512 tail; also the
+          stall of one block compression (a token that fills the tail:
+          append + compress + decode, minus a step that does not compress).
   rsvd    8 x 512 x 128 FP16 blocks of the same distribution, k=16, p=5, q=2,
           per-row INT8 quantisation; blocks/sec = matrices per second.
-Prints one JSON line.  value = algorithmic HBM bytes of one decode call
-divided by the measured time per step (GB/s); roofline.achieved uses the
+  model loop (--model-loop, separate JSON line)  transformers
+          MistralForCausalLM with Mistral-7B's shape (32 layers, hidden 4096,
+          32/8 heads, FFN 14336, vocab 32768), random FP16 weights, patched
+          with patch_unsloth_attention (k=16): 8192-token prompt, then 256
+          greedy decode steps; the same model with transformers' dense FP16
+          KV cache runs beside it.
+Prints one JSON line.  value = algorithmic HBM bytes of one headline decode
+call divided by the measured time per step (GB/s); roofline.achieved uses the
 event-timed duration of the decode call itself (partial + combine kernels).
 """
 import argparse
@@ -33,10 +43,15 @@ sys.path.insert(0, os.path.join(HERE, "unsloth-spectral_amd"))
 os.environ.setdefault("UNSLOTH_SPECTRAL_QUIET", "1")
 
 HBM_PEAK_GBS = 8000.0
-FP32_VALU_PEAK_TFLOPS = 78.6  # non-packed FP32 vector (packed FP32 is disabled in these kernels)
+MFMA_FP16_PEAK_TFLOPS = 2500.0  # dense fp16 MFMA
 
 B, HQ, HKV, D, TB, NBLK, K_RANK, TAIL = 8, 32, 8, 128, 512, 31, 32, 512
 CTX = NBLK * TB + TAIL
+
+
+def log(msg):
+    """Progress line on stderr (stdout carries only the JSON result)."""
+    print(f"[bench] {msg}", file=sys.stderr, flush=True)
 
 
 def decode_bytes(B, H, nblk, k_k, k_v, tail, per_row=True, hq=32, d=128, tb=512):
@@ -88,28 +103,53 @@ def lowrank_kv(torch, seed, n, ctx, d, device, unit_scale=False):
     return out
 
 
-def build_c3(torch, device):
-    """Tier state of the decode workload, compressed by the HIP rSVD."""
+def lowrank_kv_device(torch, seed, n, ctx, d, device, chunk=16):
+    """Same distribution as lowrank_kv, drawn on the GPU (seeded device
+    generator, QR on the device) for the large batch-16 workload."""
+    g = torch.Generator(device=device)
+    g.manual_seed(seed)
+    sig = torch.exp(-torch.arange(d, dtype=torch.float32, device=device) / 8.0)
+    out = torch.empty(n, ctx, d, dtype=torch.float16, device=device)
+    for i in range(0, n, chunk):
+        m = min(chunk, n - i)
+        U, _ = torch.linalg.qr(torch.randn(m, ctx, d, generator=g, device=device))
+        V, _ = torch.linalg.qr(torch.randn(m, d, d, generator=g, device=device))
+        out[i:i + m] = (torch.matmul(U * sig, V.transpose(1, 2).contiguous())
+                        + 0.01 * torch.randn(m, ctx, d, generator=g, device=device)).half()
+        del U, V
+    return out
+
+
+def build_decode(torch, device, b, nblk, k, tail, on_device=False, max_blocks=None):
+    """Tier state of a decode workload (b sequences, nblk cold blocks of rank
+    k, tail FP16 tokens), the cold blocks compressed by the HIP rSVD."""
     from unsloth_spectral import SpectralCache, compress_matrices
-    Kx = lowrank_kv(torch, 2, B * HKV, CTX, D, device)
-    Vx = lowrank_kv(torch, 3, B * HKV, CTX, D, device)
-    cold = NBLK * TB
+    ctx = nblk * TB + tail
+    gen = lowrank_kv_device if on_device else lowrank_kv
+    Kx = gen(torch, 2, b * HKV, ctx, D, device)
+    Vx = gen(torch, 3, b * HKV, ctx, D, device)
+    cold = nblk * TB
     tiers = []
     for X, seed in ((Kx, 4), (Vx, 5)):
-        M = X[:, :cold].reshape(B * HKV * NBLK, TB, D)
-        r = compress_matrices(M, K_RANK, seed=seed, granularity="per_row")
-        tiers.append((r["codes"].view(B, HKV, NBLK, TB, -1)[..., :K_RANK],
-                      r["scales"].view(B, HKV, NBLK, TB),
-                      r["basis"].view(B, HKV, NBLK, -1, D)[:, :, :, :K_RANK],
-                      r["minmax"].view(B, HKV, NBLK, 2)))
+        M = X[:, :cold].reshape(b * HKV * nblk, TB, D)
+        r = compress_matrices(M, k, seed=seed, granularity="per_row")
+        tiers.append((r["codes"].view(b, HKV, nblk, TB, -1)[..., :k],
+                      r["scales"].view(b, HKV, nblk, TB),
+                      r["basis"].view(b, HKV, nblk, -1, D)[:, :, :, :k],
+                      r["minmax"].view(b, HKV, nblk, 2)))
     (ck, sk, bk, mk), (cv, sv, bv, mv) = tiers
-    start = (torch.arange(NBLK, device=device) * TB)[None].expand(B, NBLK)
-    tk = Kx[:, cold:].reshape(B, HKV, TAIL, D)
-    tv = Vx[:, cold:].reshape(B, HKV, TAIL, D)
-    tp = torch.arange(cold, CTX, device=device)[None].expand(B, TAIL)
+    start = (torch.arange(nblk, device=device) * TB)[None].expand(b, nblk)
+    tk = Kx[:, cold:].reshape(b, HKV, tail, D)
+    tv = Vx[:, cold:].reshape(b, HKV, tail, D)
+    tp = torch.arange(cold, ctx, device=device)[None].expand(b, tail)
     cache = SpectralCache.from_tiers(ck, sk, bk, cv, sv, bv, start, tk, tv, tp, block_size=TB,
-                                     tail_capacity=2 * TB, minmax_k=mk, minmax_v=mv)
-    return cache, (Kx, Vx)
+                                     tail_capacity=2 * TB, minmax_k=mk, minmax_v=mv, max_blocks=max_blocks)
+    return cache, (Kx, Vx), tiers
+
+
+def build_c3(torch, device):
+    cache, raw, _ = build_decode(torch, device, B, NBLK, K_RANK, TAIL)
+    return cache, raw
 
 
 def rope_tables(torch, length, device, theta=1e6):
@@ -184,13 +224,21 @@ def bench_rsvd(torch, hip, device, reps=20):
     ms = hip.elapsed_ms(e0, e1) / reps
     r = 21
     gemm_flops = 2 * TB * D * r * (1 + 2 * 2) + 2 * r * TB * D  # M Om, 2 x (M^T Y, M Z), Q^T M
-    return M, {"blocks_per_s": round(8 / (ms * 1e-3), 1), "ms_per_call": round(ms, 4), "batch": 8,
-               "k": 16, "oversampling": 5, "n_iter": 2, "quant": "per_row",
-               "gemm_flops_per_block": gemm_flops,
-               "valu_fp32_utilisation": round(8 * gemm_flops / (ms * 1e-3) / (FP32_VALU_PEAK_TFLOPS * 1e12), 5)}
+    # reconstruction error with a fixed Gaussian sketch (the oracle uses the same one)
+    g = torch.Generator().manual_seed(8)
+    omega = torch.randn(8, D, r, generator=g)
+    res = compress_matrices(M, 16, omega=omega.to(device), granularity="per_row", debug=True)
+    Mf = M.float()
+    err = (torch.linalg.matrix_norm(Mf - torch.matmul(res["coeffs"], res["vh"])) / torch.linalg.matrix_norm(Mf))
+    return M, omega, {"blocks_per_s": round(8 / (ms * 1e-3), 1), "ms_per_call": round(ms, 4), "batch": 8,
+                      "k": 16, "oversampling": 5, "n_iter": 2, "quant": "per_row",
+                      "layer_blocks_per_s": round(8 / (ms * 1e-3) / (2 * HKV), 1),
+                      "gemm_flops_per_block": gemm_flops,
+                      "mfma_fp16_utilisation": round(8 * gemm_flops / (ms * 1e-3) / (MFMA_FP16_PEAK_TFLOPS * 1e12), 6),
+                      "recon_err": round(err.mean().item(), 6)}
 
 
-def cpu_rsvd_baseline(M_gpu):
+def cpu_rsvd_baseline(M_gpu, omega):
     import numpy as np
     from threadpoolctl import threadpool_info, threadpool_limits
     sys.path.insert(0, HERE)
@@ -208,9 +256,212 @@ def cpu_rsvd_baseline(M_gpu):
             U, S, Vh = randomized_svd_ref(M, 16, om)
             quantize_per_row(U * S[:, None, :])
             best = min(best, time.perf_counter() - t0)
+        U, S, Vh = randomized_svd_ref(M, 16, omega.numpy())
+    Mf = M.astype(np.float64)
+    err = np.linalg.norm(Mf - np.matmul(U * S[:, None, :], Vh), axis=(1, 2)) / np.linalg.norm(Mf, axis=(1, 2))
     return {"value": round(8 / best, 1), "unit": "blocks/s", "cores": max(b for b in blas if b) if blas else 1,
-            "kind": "port", "sample": "oracle randomized_svd_ref (float32 LAPACK restatement of rsvd.py) + "
-                                      f"per-row quantise, 8x512x128, k=16; best of 5 ({best * 1e3:.2f} ms)"}
+            "kind": "port", "recon_err": round(float(err.mean()), 6),
+            "sample": "oracle randomized_svd_ref (float32 LAPACK restatement of rsvd.py) + "
+                      f"per-row quantise, 8x512x128, k=16; best of 5 ({best * 1e3:.2f} ms)"}
+
+
+def time_decode(torch, lib, hip, caches, Q, cos, sin, qpos, warmup, steps):
+    """Warm-up calls, then `steps` calls bracketed by HIP events on the launch
+    stream; the tier sets in `caches` are used in rotation.  Returns
+    (ms of the whole timed loop, sorted per-call ms)."""
+    from unsloth_spectral import _lib
+    b = Q.shape[0]
+    outs = [torch.empty(b, HQ, D, dtype=torch.float16, device=Q.device) for _ in caches]
+    built = [decode_args(_lib, c, Q, o, cos, sin, qpos) for c, o in zip(caches, outs)]
+    nbytes = ctypes.c_size_t(0)
+    _lib.check(lib.sc_decode_workspace_size(ctypes.byref(built[0][0]), ctypes.byref(nbytes)))
+    ws = torch.empty(nbytes.value, dtype=torch.uint8, device=Q.device)
+    stream = ctypes.c_void_p(torch.cuda.current_stream().cuda_stream)
+
+    def step(i):
+        _lib.check(lib.sc_decode_attn(ctypes.byref(built[i % len(built)][0]), ctypes.c_void_p(ws.data_ptr()),
+                                      ws.numel(), stream))
+
+    for i in range(warmup):
+        step(i)
+    torch.cuda.synchronize()
+    starts = [hip.event() for _ in range(steps)]
+    ends = [hip.event() for _ in range(steps)]
+    torch.cuda.synchronize()
+    for i in range(steps):
+        hip.record(starts[i], stream)
+        step(i)
+        hip.record(ends[i], stream)
+    torch.cuda.synchronize()
+    total_ms = hip.elapsed_ms(starts[0], ends[-1])
+    return total_ms, sorted(hip.elapsed_ms(a, e) for a, e in zip(starts, ends))
+
+
+def compression_stall(torch, hip, cache_full, raw, reps=5):
+    """Stall of one block compression inside a decode step (batch 16 x 8 KV
+    heads, K and V: 256 rSVDs + quantisation in one launch).  A step is
+    append(one token per sequence) + decode attention, event-timed on the
+    stream; the compressing step starts from 511 tail tokens (the appended
+    token completes a block), the plain step from 510."""
+    from unsloth_spectral._decode import run_decode
+    b, nb = cache_full._B, cache_full.num_cold_blocks
+    cold = nb * TB
+    Kx, Vx = raw
+    cos, sin = rope_tables(torch, cold + 2 * TB, Kx.device)
+    g = torch.Generator(device=Kx.device)
+    g.manual_seed(11)
+    Q = torch.randn(b, HQ, 1, D, generator=g, device=Kx.device).half()
+    stream = ctypes.c_void_p(torch.cuda.current_stream().cuda_stream)
+
+    from unsloth_spectral import _lib
+
+    def with_tail(n):  # the first n tail tokens of cache_full (tail ring head at slot 0)
+        c = cache_full.clone()
+        c._tail_len = n
+        c.counters[:, _lib.SC_CNT_TAIL_LEN].fill_(n)
+        c.counters[:, _lib.SC_CNT_NEXT_POS].fill_(cold + n)
+        c.counters[:, _lib.SC_CNT_TOTAL].fill_(cold + n)
+        c.total_tokens = c.current_position = cold + n
+        return c
+
+    times = {}
+    for n in (510, 511) * (reps + 1):
+        c = with_tail(n)
+        k1 = Kx[:, cold + n:cold + n + 1].reshape(b, HKV, 1, D)
+        v1 = Vx[:, cold + n:cold + n + 1].reshape(b, HKV, 1, D)
+        torch.cuda.synchronize()
+        e0, e1 = hip.event(), hip.event()
+        hip.record(e0, stream)
+        c.append(k1, v1)
+        run_decode(Q, c, cos, sin, cold + n, rope_mode=_lib.SC_ROPE_ABSOLUTE, halves_equal=True)
+        hip.record(e1, stream)
+        ms = hip.elapsed_ms(e0, e1)
+        assert c.num_cold_blocks == nb + (n == 511)
+        times.setdefault(n, []).append(ms)
+        del c
+    med = {n: sorted(v[1:])[len(v[1:]) // 2] for n, v in times.items()}
+    return {"step_us_plain": round(med[510] * 1e3, 1), "step_us_compress": round(med[511] * 1e3, 1),
+            "stall_us": round((med[511] - med[510]) * 1e3, 1), "matrices_per_compression": 2 * b * HKV,
+            "reps": reps}
+
+
+def decode_config(torch, lib, hip, device, b, nblk, k, tail, rotate, warmup, steps, on_device=False,
+                  stall=False):
+    """One secondary decode workload: event-timed call duration and the HBM
+    roofline fraction of its algorithmic bytes."""
+    log(f"building batch {b}, {nblk} cold blocks k={k}")
+    cache0, raw, _ = build_decode(torch, device, b, nblk, k, tail, on_device=on_device,
+                                  max_blocks=nblk + 1 if stall else None)
+    ctx = nblk * TB + tail
+    caches = [cache0] + [cache0.clone() for _ in range(rotate - 1)]
+    cos, sin = rope_tables(torch, ctx + 64, device)
+    g = torch.Generator(device=device)
+    g.manual_seed(1)
+    Q = torch.randn(b, HQ, D, generator=g, device=device).half()
+    total_ms, per_call = time_decode(torch, lib, hip, caches, Q, cos, sin, ctx - 1, warmup, steps)
+    avg = sum(per_call) / len(per_call)
+    nbytes = decode_bytes(b, HKV, nblk, k, k, tail)
+    ach = nbytes / (avg * 1e-3) / 1e9
+    res = {"batch": b, "context": ctx, "cold_blocks": nblk, "rank": k, "tail": tail, "tier_sets_rotated": rotate,
+           "steps": steps, "warmup": warmup, "us_per_layer": round(avg * 1e3, 2),
+           "us_per_layer_median": round(per_call[len(per_call) // 2] * 1e3, 2),
+           "algorithmic_bytes_per_call": nbytes,
+           "roofline": {"bound": "hbm", "achieved": round(ach, 2), "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                        "frac": round(ach / HBM_PEAK_GBS, 4)}}
+    del caches
+    log(f"batch {b}: {avg * 1e3:.2f} us per call")
+    if stall:
+        res["compression_stall"] = compression_stall(torch, hip, cache0, raw)
+        log(f"compression stall: {res['compression_stall']}")
+    del cache0, raw
+    torch.cuda.empty_cache()
+    return res
+
+
+def model_loop(torch, device, prompt, decode_steps, layers=32):
+    """Mistral-7B-shaped transformers model (random FP16 weights): prefill of
+    `prompt` tokens, then `decode_steps` greedy one-token steps, with the
+    spectral cache (patch_unsloth_attention, k=16) and, on the same weights,
+    with transformers' dense FP16 KV cache.  Tokens/s of the decode phase."""
+    from transformers import MistralConfig, MistralForCausalLM
+    from unsloth_spectral import get_cache_stats, patch_unsloth_attention
+    cfg = MistralConfig(vocab_size=32768, hidden_size=4096, intermediate_size=14336, num_hidden_layers=layers,
+                        num_attention_heads=32, num_key_value_heads=8, head_dim=128,
+                        max_position_embeddings=32768, rope_theta=1e6, sliding_window=None, rms_norm_eps=1e-5)
+    cfg._attn_implementation = "sdpa"
+    torch.manual_seed(0)
+    t0 = time.perf_counter()
+    with torch.device(device):
+        model = MistralForCausalLM._from_config(cfg, dtype=torch.float16).eval()
+    torch.cuda.synchronize()
+    init_s = time.perf_counter() - t0
+    log(f"model built in {init_s:.1f} s")
+    g = torch.Generator().manual_seed(12)
+    ids = torch.randint(0, cfg.vocab_size, (1, prompt), generator=g).to(device)
+
+    def timed(fn):
+        torch.cuda.synchronize()
+        t = time.perf_counter()
+        r = fn()
+        torch.cuda.synchronize()
+        return r, time.perf_counter() - t
+
+    @torch.no_grad()
+    def dense_run(n_prompt, steps):
+        out = model(input_ids=ids[:, :n_prompt], use_cache=True, logits_to_keep=1)
+        past, tok = out.past_key_values, out.logits[:, -1].argmax(-1)
+        torch.cuda.synchronize()
+        t = time.perf_counter()
+        for _ in range(steps):
+            out = model(input_ids=tok[:, None], past_key_values=past, use_cache=True, logits_to_keep=1)
+            past, tok = out.past_key_values, out.logits[:, -1].argmax(-1)
+        torch.cuda.synchronize()
+        return time.perf_counter() - t
+
+    @torch.no_grad()
+    def spectral_run(n_prompt, steps):
+        for layer in model.model.layers:
+            layer.self_attn._spectral_cache = None
+        out, pre_s = timed(lambda: model(input_ids=ids[:, :n_prompt], use_cache=False, logits_to_keep=1))
+        tok = out.logits[:, -1].argmax(-1)
+        torch.cuda.synchronize()
+        t = time.perf_counter()
+        for i in range(steps):
+            pos = torch.tensor([[n_prompt + i]], device=device)
+            out = model(input_ids=tok[:, None], position_ids=pos, use_cache=False, logits_to_keep=1)
+            tok = out.logits[:, -1].argmax(-1)
+        torch.cuda.synchronize()
+        return pre_s, time.perf_counter() - t
+
+    dense_run(min(prompt, 1024), 4)                      # warm-up (kernels, allocator)
+    dense_s = dense_run(prompt, decode_steps)
+    log(f"dense KV cache: {dense_s / decode_steps * 1e3:.2f} ms per token")
+    torch.cuda.empty_cache()
+    patch_unsloth_attention(model, k_rank_keys=16, k_rank_values=16, verbose=False, quant_granularity="per_row")
+    spectral_run(min(prompt, 1024) + 8, 4)
+    prefill_s, spec_s = spectral_run(prompt, decode_steps)
+    log(f"spectral cache: {spec_s / decode_steps * 1e3:.2f} ms per token, prefill {prefill_s:.2f} s")
+    st = get_cache_stats(model)
+    return {
+        "metric": "model decode tokens/s (spectral cache vs dense fp16 KV cache)",
+        "value": round(decode_steps / spec_s, 2), "unit": "tokens/s", "n_gpus": 1, "steps": decode_steps,
+        "warmup": 4, "ms_per_step": round(spec_s / decode_steps * 1e3, 3), "higher_is_better": True,
+        "scaling": "weak", "vs_baseline": None, "dtype": "fp16", "data": "synthetic",
+        "config": {"workload": f"transformers MistralForCausalLM, Mistral-7B shape ({layers} layers, hidden 4096, "
+                               "32/8 heads, head_dim 128, FFN 14336, vocab 32768), random fp16 weights; "
+                               f"{prompt}-token prompt + {decode_steps} greedy steps, batch 1; spectral cache k=16 "
+                               "(K and V), per-row INT8 scales, absolute RoPE theta 1e6",
+                   "prompt": prompt, "decode_steps": decode_steps, "layers": layers},
+        "spectral": {"decode_ms_per_token": round(spec_s / decode_steps * 1e3, 3),
+                     "prefill_s": round(prefill_s, 3),
+                     "cold_blocks_per_layer": st["total_blocks"] // layers,
+                     "compressions_during_decode": (prompt + decode_steps) // TB - prompt // TB,
+                     "kv_bytes": st["total_compressed_bytes"], "kv_bytes_fp16": st["total_original_bytes"],
+                     "compression_ratio": round(st["compression_ratio"], 3)},
+        "dense_fp16_kv": {"decode_ms_per_token": round(dense_s / decode_steps * 1e3, 3),
+                          "tokens_per_s": round(decode_steps / dense_s, 2)},
+        "model_init_s": round(init_s, 1),
+    }
 
 
 TRAFFIC_JSON = os.path.join(HERE, "profiles", "decode_c3_traffic.json")
@@ -300,6 +551,12 @@ def main():
     ap.add_argument("--warmup", type=int, default=3000)  # ~0.15 s: GPU clocks settle before timing
     ap.add_argument("--rotate", type=int, default=4)
     ap.add_argument("--no-cpu", action="store_true")
+    ap.add_argument("--only-headline", action="store_true",
+                    help="time only the batch-8 decode workload and the rSVD (profiling runs)")
+    ap.add_argument("--model-loop", action="store_true",
+                    help="run the Mistral-7B-shaped model loop instead and print its JSON line")
+    ap.add_argument("--prompt", type=int, default=8192)
+    ap.add_argument("--decode-steps", type=int, default=256)
     ap.add_argument("--copy-probe-mib", type=int, default=0,
                     help="run a plain copy kernel of this size first (counter calibration)")
     ap.add_argument("--summarize-pmc", nargs=2, metavar=("FETCH_DIR", "WRITE_DIR"),
@@ -319,40 +576,22 @@ def main():
     torch.cuda.set_device(device)
     lib = _lib.load()
     hip = Hip()
+    if args.model_loop:
+        print(json.dumps(model_loop(torch, device, args.prompt, args.decode_steps)))
+        return
     if args.copy_probe_mib:
         copy_probe(torch, device, args.copy_probe_mib)
 
+    log("building the batch-8 16K tiers")
     cache0, raw = build_c3(torch, device)
     del raw
+    log("timing decode, batch 8")
     caches = [cache0] + [cache0.clone() for _ in range(args.rotate - 1)]
     cos, sin = rope_tables(torch, CTX + 64, device)
     g = torch.Generator(device=device)
     g.manual_seed(1)
     Q = torch.randn(B, HQ, D, generator=g, device=device).half()
-    outs = [torch.empty(B, HQ, D, dtype=torch.float16, device=device) for _ in caches]
-    built = [decode_args(_lib, c, Q, o, cos, sin, CTX - 1) for c, o in zip(caches, outs)]
-    nbytes = ctypes.c_size_t(0)
-    _lib.check(lib.sc_decode_workspace_size(ctypes.byref(built[0][0]), ctypes.byref(nbytes)))
-    ws = torch.empty(nbytes.value, dtype=torch.uint8, device=device)
-    stream = ctypes.c_void_p(torch.cuda.current_stream().cuda_stream)
-
-    def step(i):
-        _lib.check(lib.sc_decode_attn(ctypes.byref(built[i % len(built)][0]), ctypes.c_void_p(ws.data_ptr()),
-                                      ws.numel(), stream))
-
-    for i in range(args.warmup):
-        step(i)
-    torch.cuda.synchronize()
-    starts = [hip.event() for _ in range(args.steps)]
-    ends = [hip.event() for _ in range(args.steps)]
-    torch.cuda.synchronize()
-    for i in range(args.steps):
-        hip.record(starts[i], stream)
-        step(i)
-        hip.record(ends[i], stream)
-    torch.cuda.synchronize()
-    total_ms = hip.elapsed_ms(starts[0], ends[-1])
-    per_call = sorted(hip.elapsed_ms(s, e) for s, e in zip(starts, ends))
+    total_ms, per_call = time_decode(torch, lib, hip, caches, Q, cos, sin, CTX - 1, args.warmup, args.steps)
     avg_call_ms = sum(per_call) / len(per_call)
     med_call_ms = per_call[len(per_call) // 2]
     ms_per_step = total_ms / args.steps
@@ -361,12 +600,26 @@ def main():
     achieved = nb / (avg_call_ms * 1e-3) / 1e9
     traffic = load_traffic()
 
-    M_rsvd, rsvd = bench_rsvd(torch, hip, device)
+    log(f"decode batch 8: {avg_call_ms * 1e3:.2f} us per call; timing rSVD")
+    M_rsvd, omega, rsvd = bench_rsvd(torch, hip, device)
     cpu = cpu_rsvd = None
     if not args.no_cpu:
+        log("CPU baselines (oracle)")
         cpu = cpu_decode_baseline(cache0, Q.view(B, HQ, D), cos, sin)
-        cpu_rsvd = cpu_rsvd_baseline(M_rsvd)
+        cpu_rsvd = cpu_rsvd_baseline(M_rsvd, omega)
         rsvd["cpu_baseline"] = cpu_rsvd
+        rsvd["recon_err_rel_diff_vs_oracle"] = round(abs(rsvd["recon_err"] - cpu_rsvd["recon_err"])
+                                                     / cpu_rsvd["recon_err"], 5)
+    others = None
+    if not args.only_headline:
+        del caches, cache0
+        torch.cuda.empty_cache()
+        log("decode batch 1 (4K) and batch 16 (33K, with compression stall)")
+        others = {
+            "batch1_ctx4096": decode_config(torch, lib, hip, device, 1, 7, 16, 512, args.rotate, 1000, 200),
+            "batch16_ctx33280": decode_config(torch, lib, hip, device, 16, 64, 32, 512, 2, 300, 100,
+                                              on_device=True, stall=True),
+        }
     res = {
         "metric": "decode attn µs/layer + HBM GB/s (% peak) at 16K ctx; rSVD blocks/sec",
         "value": round(nb / (ms_per_step * 1e-3) / 1e9, 2),
@@ -395,6 +648,7 @@ def main():
                      "kernel": "sc_decode_attn call (decode_partial_kernel + decode_combine_kernel)"},
         "cpu_baseline": cpu,
         "rsvd": rsvd,
+        "other_decode_workloads": others,
     }
     print(json.dumps(res))
 

@@ -31,7 +31,7 @@
 extern "C" {
 #endif
 
-#define SC_ABI_VERSION 1
+#define SC_ABI_VERSION 2
 
 #define SC_OK 0
 #define SC_ERR_INVALID (-1)      /* bad argument / shape */
@@ -121,6 +121,14 @@ typedef struct ScTierDesc {
  *              (>= every counters[b][SC_CNT_TAIL_LEN]).
  * halves_equal != 0 asserts cos[:, :D/2] == cos[:, D/2:] (HF tables) and
  * lets the kernel read half rows.
+ * split: workgroups per cold block, a power of two dividing block_size/64
+ *   (each takes that share of the block's 64-token ranges); 0 = chosen from
+ *   the grid size (small batches split their blocks to fill the GPU).  The
+ *   split sets the order in which partial results are summed: results with
+ *   equal splits are bit-identical for a sequence whatever else is in the
+ *   batch; different splits agree to fp32 rounding.  The reference's
+ *   TritonSpectralConfig (kernels/spectral_attention.py:50-65) is its
+ *   launch-configuration counterpart.
  */
 typedef struct ScDecodeArgs {
   const ScTierDesc* tier;
@@ -144,6 +152,7 @@ typedef struct ScDecodeArgs {
   int64_t out_stride_b, out_stride_h;
   float* logits_out;
   int64_t logits_stride_b, logits_stride_h;
+  int32_t split;
 } ScDecodeArgs;
 
 int sc_decode_workspace_size(const ScDecodeArgs* args, size_t* bytes);

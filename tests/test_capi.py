@@ -35,7 +35,7 @@ def test_library_exports_every_declared_symbol():
     for fn in _declared_functions():
         assert hasattr(lib, fn), fn
     assert set(_lib.PROTOTYPES) == _declared_functions()
-    assert _lib.load().sc_abi_version() == 1
+    assert _lib.load().sc_abi_version() == _lib.ABI_VERSION == 2
 
 
 def test_struct_layouts_match_header():

@@ -20,7 +20,8 @@ ATOL = 2e-3
 RTOL_MAX = 1e-2
 
 
-def _run(states, Q16, cos, sin, q, mode, mask=None, block_size=None, qpos_tensor=False):
+def _run(states, Q16, cos, sin, q, mode, mask=None, block_size=None, qpos_tensor=False, split=0,
+         with_logits=True):
     from unsloth_spectral import _lib
     from unsloth_spectral._decode import run_decode
     cache = cache_from_states(states, block_size)
@@ -28,13 +29,13 @@ def _run(states, Q16, cos, sin, q, mode, mask=None, block_size=None, qpos_tensor
     total = states[0].total_tokens()
     ct, st = tables(cos, sin)
     Q = torch.from_numpy(Q16).cuda().reshape(B, Hq, 1, D)
-    logits = torch.full((B, Hq, total), float("nan"), dtype=torch.float32, device="cuda")
+    logits = torch.full((B, Hq, total), float("nan"), dtype=torch.float32, device="cuda") if with_logits else None
     m = None if mask is None else torch.from_numpy(mask).cuda()
     qp = torch.tensor(q, dtype=torch.int32, device="cuda") if qpos_tensor else q
     code = _lib.SC_ROPE_ABSOLUTE if mode == "absolute" else _lib.SC_ROPE_DISTANCE
-    out = run_decode(Q, cache, ct, st, qp, m, None, code, logits=logits)
+    out = run_decode(Q, cache, ct, st, qp, m, None, code, logits=logits, split=split)
     torch.cuda.synchronize()
-    return out[:, :, 0].float().cpu().numpy(), logits.cpu().numpy()
+    return out[:, :, 0].float().cpu().numpy(), (logits.cpu().numpy() if with_logits else None)
 
 
 def _ulp16(x):
@@ -167,9 +168,41 @@ def test_c3_geometry_full_batch():
     cos, sin = rope_tables(16384 + 64, 128)
     Q = rng.standard_normal((8, 32, 128)).astype(np.float16)
     out, logits = _check(states, Q, cos, sin, 16383, "absolute", seqs=[0, 7])
-    # batch invariance: sequence 3 alone == sequence 3 in the batch
-    out1, logits1 = _run([states[3]], Q[3:4], cos, sin, 16383, "absolute")
+    # batch invariance at a fixed split: sequence 3 alone == sequence 3 in
+    # the batch (batch 8 fills the GPU unsplit; batch 1 alone would split)
+    out1, logits1 = _run([states[3]], Q[3:4], cos, sin, 16383, "absolute", split=1)
     np.testing.assert_array_equal(out1[0], out[3])
+    np.testing.assert_array_equal(logits1[0], logits[3])
+
+
+@pytest.mark.parametrize("with_logits", [False, True])
+def test_block_split_variants(with_logits):
+    """A cold block split over 1, 2, 4 or 8 workgroups (64-token ranges
+    each) gives the oracle's result; splits differ from each other only in
+    where partial sums are rounded (each workgroup's record is merged in
+    fp32 and the output rounded once to fp16): within a few fp16 ulps of
+    the largest output.  Without
+    logits this is the branch-free path, with logits the general one."""
+    from unsloth_spectral._lib import SpectralHIPError
+    rng = np.random.default_rng(14)
+    states = [random_state(rng, 8, 128, 3, 512, 32, 32, 200, per_row=True) for _ in range(2)]
+    total = states[0].total_tokens()
+    cos, sin = rope_tables(total + 16, 128)
+    Q = rng.standard_normal((2, 32, 128)).astype(np.float16)
+    outs = {}
+    for split in (1, 2, 4, 8, 0):
+        out, lg = _run(states, Q, cos, sin, total - 1, "absolute", split=split, with_logits=with_logits)
+        outs[split] = out
+        for b in range(2):
+            ref, _, logits16 = o_abs(Q[b], states[b], cos, sin, total - 1)
+            assert np.abs(out[b] - ref).max() <= ATOL, (split, b)
+            if with_logits:
+                assert pearson(lg[b].ravel(), logits16.ravel()) >= 0.9999
+        diff = np.abs(out - outs[1]).max()
+        assert diff <= 4 * _ulp16(np.abs(outs[1]).max()), (split, diff)
+    assert np.array_equal(outs[0], outs[8])   # 2 sequences x 2 head groups x 3 blocks: auto splits 8 ways
+    with pytest.raises(SpectralHIPError):
+        _run(states, Q, cos, sin, total - 1, "absolute", split=3, with_logits=with_logits)
 
 
 def test_rope_none_equals_dense_unrotated():

@@ -44,6 +44,7 @@ constexpr int kWaves = 4;
 constexpr int kThreads = 64 * kWaves;
 constexpr int kTile = 16;
 constexpr int kMaxRep = 16;
+constexpr long kFillUnits = 512;  // two resident workgroups per CU on 256 CUs
 constexpr int kVRow = 132;                              // LDS row (halves) of a staged V tile
 constexpr int kCombineWaves = 4;  // waves (query heads) per combine workgroup
 constexpr float kLog2e = 1.4426950408889634f;
@@ -51,6 +52,7 @@ constexpr float kLog2e = 1.4426950408889634f;
 struct DecodeParams {
   int B, Hq, Hkv, nrep, TB, NB, TCAP, per_row, rope_mode, rope_len, halves_equal;
   int grid_blocks, tpw, n_hq, cold_units, units_per_bh, fold_tail;
+  int split;  // workgroups per cold block (each takes TB / (64 * split) consecutive ranges)
   long n_cold_units;  // summed over (b, head group)
   float scale;
   const h16* q;
@@ -880,7 +882,10 @@ __device__ void cold_unit(const DecodeParams& p, int b, int hq, int j, char* sme
   const Lanes lr = lane_roles<ONE>(n, nrep);
   const int qhead = ONE ? n >> 2 : n;  // query head of this lane's MFMA column
   const int ncold = p.counters[b * SC_NCOUNTERS + SC_CNT_NCOLD];
-  if (j >= ncold) {  // uniform over the workgroup: no cold block, tail tiles only
+  const int jb = j / p.split;                  // cold block of this unit
+  const int nR = p.TB / T / p.split;           // ranges of this unit
+  const int r0 = (j - jb * p.split) * nR;      // its first range within the block
+  if (jb >= ncold) {  // uniform over the workgroup: no cold block, tail tiles only
     if (!hvalid) return;
     half8_t qt[G::DS];
     if (lr.valid) {
@@ -914,26 +919,25 @@ __device__ void cold_unit(const DecodeParams& p, int b, int hq, int j, char* sme
     write_record<D, ONE>(p, b, h, j, lr, oacc, sm.m2, head_sum<ONE>(sm.l));
     return;
   }
-  const long bhj = (long)(b * p.Hkv + (hvalid ? h : 0)) * p.NB + j;
-  const int start = p.block_start[b * p.NB + j];
+  const long bhj = (long)(b * p.Hkv + (hvalid ? h : 0)) * p.NB + jb;
+  const int start = p.block_start[b * p.NB + jb];
   const int qp = p.qpos ? p.qpos[b] : p.qpos_scalar;
   const bool dist = p.rope_mode == SC_ROPE_DISTANCE;
   const bool rope = !GEN || p.rope_mode != SC_ROPE_NONE;
-  const int R = p.TB / T;  // ranges per block
   constexpr int RBUF = T * RS::ROW;  // bytes of one staged range
 
   // ---- prologue: RoPE rows of range 0 (L2) first, then the HBM loads
   using SM = StageMap<D, HE, T>;
   const SM smap = stage_map<D, HE, T>(p, dist);
   U4s<2 * SM::NS> sv0{};  // range 0's RoPE rows: requested before the HBM loads, stored after them
-  if (rope) sv0 = stage_fetch<D, HE, T>(p, smap, start, qp, dist);
+  if (rope) sv0 = stage_fetch<D, HE, T>(p, smap, start + r0 * T, qp, dist);
   CB cb0;  // codes of the current range, refilled in place with the next
   half8_t a8[G::MT][KC];
   half4_t a4[G::MT];
   half8_t qb[G::DS];
   float vn = 1.f;
   if (hvalid) {
-    load_codes<KK, PRM, ONE>(p, code_src<KK, KV>(p, bhj, 0), cb0);
+    load_codes<KK, PRM, ONE>(p, code_src<KK, KV>(p, bhj, r0 * T), cb0);
     // K basis as the A operand: row n of tile mt is d = perm(mt, n).
     const h16* bk = p.basis_k + bhj * (long)D * KK;
 #pragma unroll
@@ -956,7 +960,7 @@ __device__ void cold_unit(const DecodeParams& p, int b, int hq, int j, char* sme
     vn = p.vnorm[bhj];
   }
   if (rope) stage_store<D, HE, T>(smem, smap, sv0);
-  const long cache_tok = (long)j * p.TB;  // cache-order index of the block's first token
+  const long cache_tok = (long)jb * p.TB + r0 * T;  // cache-order index of the unit's first token
   const uint8_t* mrow = nullptr;
   float* lrow = nullptr;
   if constexpr (GEN) {
@@ -983,25 +987,25 @@ __device__ void cold_unit(const DecodeParams& p, int b, int hq, int j, char* sme
     char* next = smem + ((rr + 1) & 1) * RBUF;
     if (hvalid) {
       RangeLogits<ONE, TPW> lg;
-      range_scores<D, KK, KV, TPW, GEN, HE, PRM, M>(p, cb0, code_src<KK, KV>(p, bhj, (rr + 1) * T), a8, a4, qb, smap,
-                                                     cur, next, start + (rr + 1) * T, qp, dist, rope,
+      range_scores<D, KK, KV, TPW, GEN, HE, PRM, M>(p, cb0, code_src<KK, KV>(p, bhj, (r0 + rr + 1) * T), a8, a4, qb,
+                                                     smap, cur, next, start + (r0 + rr + 1) * T, qp, dist, rope,
                                                      mrow ? mrow + rr * T : nullptr, lrow ? lrow + rr * T : nullptr,
                                                      lg);
       if constexpr (P)
-        range_values<KV, TPW, GEN, PRM, true>(p, cb0, code_src<KK, KV>(p, bhj, rr * T), lgp, msp, alp, vn, st);
+        range_values<KV, TPW, GEN, PRM, true>(p, cb0, code_src<KK, KV>(p, bhj, (r0 + rr) * T), lgp, msp, alp, vn, st);
       range_max<ONE, TPW>(lg, st, msp, alp);
       lgp = lg;
     } else if (M && rope) {
       // idle head slot: still stage its share of the next range's rows
-      stage_store<D, HE, T>(next, smap, stage_fetch<D, HE, T>(p, smap, start + (rr + 1) * T, qp, dist));
+      stage_store<D, HE, T>(next, smap, stage_fetch<D, HE, T>(p, smap, start + (r0 + rr + 1) * T, qp, dist));
     }
     __syncthreads();
   };
   using TT = std::integral_constant<bool, true>;
   using FF = std::integral_constant<bool, false>;
-  if (R > 1) {
+  if (nR > 1) {
     step(TT(), FF(), 0);
-    for (int rr = 1; rr + 1 < R; ++rr) step(TT(), TT(), rr);
+    for (int rr = 1; rr + 1 < nR; ++rr) step(TT(), TT(), rr);
   }
   // the first FP16 tail tile of this workgroup is loaded during the last range
   TailFetch<D> tf;
@@ -1016,8 +1020,8 @@ __device__ void cold_unit(const DecodeParams& p, int b, int hq, int j, char* sme
 #pragma unroll
     for (int nt = 0; nt < NT; ++nt)
       bvf[mt][nt] = *reinterpret_cast<const half4_t*>(bvb + (long)(16 * mt + n) * KV + 16 * nt + 4 * g);
-  if (R > 1)
-    step(FF(), TT(), R - 1);
+  if (nR > 1)
+    step(FF(), TT(), nR - 1);
   else
     step(FF(), FF(), 0);
   tail_fetch_rope<D, HE>(p, rope, tf);  // positions arrived during the last range (unconditional: no branch)
@@ -1202,7 +1206,19 @@ int fill_params(const ScDecodeArgs* a, DecodeParams* p) {
   // do tail work, and no workgroup gets more than one tail tile.
   const int tail_tiles_grid = (a->grid_tail + kTile - 1) / kTile;
   p->fold_tail = a->grid_tail > 0;
-  p->cold_units = p->grid_blocks > tail_tiles_grid ? p->grid_blocks : tail_tiles_grid;
+  // A cold block is split over `split` workgroups (consecutive 64-token
+  // ranges each) while the grid holds fewer than kFillUnits workgroups:
+  // small batches would otherwise leave most CUs idle while a few
+  // workgroups walk whole blocks.
+  const int ranges = t->block_size / (kTile * tpw);
+  const long base_units = (long)a->grid_blocks * t->batch * ((t->kv_heads + kWaves - 1) / kWaves);
+  if (a->split < 0 || ranges % (a->split > 0 ? a->split : 1) || (a->split & (a->split - 1)))
+    return sc_fail(SC_ERR_INVALID, "split %d must be a power of two dividing block_size/64 = %d", a->split, ranges);
+  p->split = a->split > 0 ? a->split : 1;
+  if (a->split == 0)
+    while (ranges % (2 * p->split) == 0 && base_units * p->split * 2 <= kFillUnits) p->split *= 2;
+  const int split_units = p->grid_blocks * p->split;
+  p->cold_units = split_units > tail_tiles_grid ? split_units : tail_tiles_grid;
   p->units_per_bh = p->cold_units;
   p->n_cold_units = (long)p->cold_units * p->B * p->n_hq;
   p->scale = a->scale;

@@ -50,12 +50,13 @@ def as_cache(cache):
 
 
 def run_decode(Q, cache, cos, sin, query_position, attention_mask=None, scale=None,
-               rope_mode=_lib.SC_ROPE_ABSOLUTE, logits=None, halves_equal=None):
+               rope_mode=_lib.SC_ROPE_ABSOLUTE, logits=None, halves_equal=None, split=0):
     """Q [B, Hq, 1, D] post-RoPE query -> [B, Hq, 1, D] in Q.dtype.
 
     ``logits`` (optional fp32 [B, Hq, T_total]) receives score*scale in cache
     order.  ``attention_mask`` is a keep-mask broadcastable to [B, Hq, 1, T]
-    (entries equal to 0 are dropped, spectral_attention.py:284-285)."""
+    (entries equal to 0 are dropped, spectral_attention.py:284-285).
+    ``split`` = workgroups per cold block (0 = chosen from the grid size)."""
     _lib.require_device(Q, "Q")
     if Q.dim() != 4 or Q.shape[2] != 1:
         raise ValueError(f"decode attention takes one query token: Q must be [B, H, 1, D], got {tuple(Q.shape)}")
@@ -87,6 +88,7 @@ def run_decode(Q, cache, cos, sin, query_position, attention_mask=None, scale=No
     a.grid_blocks = cache._n_cold
     a.grid_tail = cache._tail_len
     a.scale = float(scale)
+    a.split = int(split)
     a.q = q.data_ptr()
     a.q_stride_b, a.q_stride_h = q.stride(0), q.stride(1)
     keep = []

@@ -12,6 +12,7 @@ import torch
 _HERE = os.path.dirname(os.path.abspath(__file__))
 LIB_PATH = os.path.join(_HERE, "libspectral_hip.so")
 
+ABI_VERSION = 2  # SC_ABI_VERSION of include/spectral_hip.h
 SC_OK = 0
 SC_ROPE_ABSOLUTE, SC_ROPE_DISTANCE, SC_ROPE_NONE = 0, 1, 2
 SC_QUANT_PER_HEAD, SC_QUANT_PER_ROW, SC_QUANT_PER_TENSOR = 0, 1, 2
@@ -49,6 +50,7 @@ class ScDecodeArgs(ctypes.Structure):
         ("mask", c_vp), ("mask_stride_b", c_i64), ("mask_stride_h", c_i64),
         ("out", c_vp), ("out_stride_b", c_i64), ("out_stride_h", c_i64),
         ("logits_out", c_vp), ("logits_stride_b", c_i64), ("logits_stride_h", c_i64),
+        ("split", c_i32),
     ]
 
 
@@ -101,7 +103,7 @@ def load():
                 fn = getattr(lib, name)
                 fn.restype = res
                 fn.argtypes = args
-            if lib.sc_abi_version() != 1:
+            if lib.sc_abi_version() != ABI_VERSION:
                 raise ImportError("libspectral_hip.so ABI version mismatch")
             _lib = lib
     return _lib

@@ -92,21 +92,35 @@ def _model_rope(module, head_dim):
     return tab
 
 
-def _dense_prefill(q_rot, cache, cos_tab, sin_tab, n_rep, attention_mask, scale):
-    """Dense causal attention over get_kv() with keys rotated at their
-    absolute positions (integration.py:297-346)."""
+def _dense_prefill(q_rot, cache, cos_tab, sin_tab, n_rep, attention_mask, scale, q_pos, rows=1024):
+    """Dense attention over get_kv() with keys rotated at their absolute
+    positions (integration.py:297-346): fp16 scores, additive mask, softmax
+    in fp32 cast back to fp16, fp16 P.V.  Causality comes from the positions
+    (key position <= query position), so a prompt appended in several chunks
+    sees the right keys; an additive float mask of matching shape is added
+    as well.  Query rows are processed in slices of ``rows`` to bound the
+    [Hq, rows, L] score buffer.  Both products take contiguous operands."""
     K, V = cache.get_kv()
     pos = cache.get_all_positions()
     K = apply_rope(K, cos_tab[pos][None, None], sin_tab[pos][None, None])
-    K = _repeat_kv(K, n_rep)
-    V = _repeat_kv(V, n_rep)
-    T, L = q_rot.shape[2], K.shape[2]
+    Kt = _repeat_kv(K, n_rep).transpose(2, 3).contiguous()
+    V = _repeat_kv(V, n_rep).contiguous()
+    T, L = q_rot.shape[2], Kt.shape[3]
+    extra = None
     if attention_mask is not None and attention_mask.dim() == 4 and attention_mask.shape[-1] == L \
-            and attention_mask.dtype != torch.bool:
-        mask = attention_mask[..., -T:, :].to(q_rot.dtype)
-        return F.scaled_dot_product_attention(q_rot, K, V, attn_mask=mask, scale=scale)
-    causal = torch.ones(T, L, dtype=torch.bool, device=q_rot.device).tril(L - T)
-    return F.scaled_dot_product_attention(q_rot, K, V, attn_mask=causal, scale=scale)
+            and attention_mask.shape[-2] >= T and attention_mask.is_floating_point():
+        extra = attention_mask[..., -T:, :]
+    out = torch.empty_like(q_rot)
+    for r0 in range(0, T, rows):
+        r1 = min(T, r0 + rows)
+        w = torch.matmul(q_rot[:, :, r0:r1].contiguous(), Kt) * scale
+        keep = pos[None, :] <= q_pos[0, r0:r1, None]
+        w = w.masked_fill(~keep, float("-inf"))
+        if extra is not None:
+            w = w + extra[..., r0:r1, :].to(w.dtype)
+        p = F.softmax(w, dim=-1, dtype=torch.float32).to(q_rot.dtype)
+        out[:, :, r0:r1] = torch.matmul(p, V)
+    return out
 
 
 def _cache_for(module, num_kv, head_dim, dtype, device, opts):
@@ -147,7 +161,7 @@ def _attend(self, hidden_states, cos_cur, sin_cur, position_ids, attention_mask,
         qpos = position_ids[:, -1]
         out = run_decode(q_rot, cache, cos_tab, sin_tab, qpos, None, scale, rope_mode, halves_equal=True)
     else:
-        out = _dense_prefill(q_rot, cache, cos_tab, sin_tab, Hq // Hkv, attention_mask, scale)
+        out = _dense_prefill(q_rot, cache, cos_tab, sin_tab, Hq // Hkv, attention_mask, scale, position_ids)
     out = out.to(hidden_states.dtype).transpose(1, 2).reshape(B, T, Hq * D)
     return self.o_proj(out), cache
 

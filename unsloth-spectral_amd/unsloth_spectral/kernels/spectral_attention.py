@@ -23,15 +23,19 @@ from ..spectral_cache import SpectralCache
 
 @dataclass
 class TritonSpectralConfig:
-    """Launch knobs of the reference's Triton kernels (:50-65).  Accepted for
-    API compatibility; the HIP kernel's tiling is fixed (16-token MFMA tiles,
-    four wavefronts per block) and nothing is logged per block."""
+    """Launch knobs of the reference's Triton kernels (:50-65).  The tile
+    fields are accepted for API compatibility; the HIP kernel's tiling is
+    fixed (16-token MFMA tiles, 64-token ranges, four wavefronts per
+    workgroup) and nothing is logged per block.  ``split_blocks`` is this
+    kernel's one launch knob: workgroups per cold block (0 = chosen from the
+    grid size; fix it to get bit-identical results across batch sizes)."""
     BLOCK_T: int = 64
     BLOCK_K: int = 32
     BLOCK_D: int = 64
     num_warps: int = 4
     num_stages: int = 2
     enable_logging: bool = True
+    split_blocks: int = 0
 
     def __post_init__(self):
         assert self.BLOCK_T >= 16, "BLOCK_T must be at least 16"
@@ -63,7 +67,8 @@ def spectral_attention_decode(
 ) -> torch.Tensor:
     """Decode attention over the spectral cache, absolute-RoPE alignment.
     Q [B, H_q, 1, D] post-RoPE -> [B, H_q, 1, D]."""
-    return run_decode(Q, cache, cos, sin, query_position, attention_mask, scale, _lib.SC_ROPE_ABSOLUTE)
+    return run_decode(Q, cache, cos, sin, query_position, attention_mask, scale, _lib.SC_ROPE_ABSOLUTE,
+                      split=config.split_blocks if config is not None else 0)
 
 
 def _one_block_cache(coeffs, basis, start_position, kind, D, B):

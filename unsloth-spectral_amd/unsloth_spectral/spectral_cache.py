@@ -417,13 +417,15 @@ class SpectralCache:
     @classmethod
     def from_tiers(cls, codes_k, scales_k, basis_k, codes_v, scales_v, basis_v, block_start,
                    tail_k=None, tail_v=None, tail_pos=None, *, block_size=None, tail_capacity=None,
-                   minmax_k=None, minmax_v=None, seed=0):
+                   minmax_k=None, minmax_v=None, seed=0, max_blocks=None):
         """Builds a cache from explicit tiers (the reference builds tier states
         only by appending; configs with a 448+64-token tail need them built
         directly).  Layouts (B sequences, H KV heads, NB blocks, T tokens):
           codes_k/v  int8 [B, H, NB, T, k]     scales_k/v  f32 [B, H, NB] or [B, H, NB, T]
           basis_k/v  f16  [B, H, NB, k, D]     block_start int [B, NB]
-          tail_k/v   f16  [B, H, Tt, D] (pre-RoPE)   tail_pos int [B, Tt]"""
+          tail_k/v   f16  [B, H, Tt, D] (pre-RoPE)   tail_pos int [B, Tt]
+        ``max_blocks`` reserves cold-tier room beyond NB (later compressions
+        then reuse it instead of growing the tier buffers)."""
         B, H, NB, T, kK = codes_k.shape
         kV = codes_v.shape[-1]
         D = basis_k.shape[-1]
@@ -431,7 +433,7 @@ class SpectralCache:
         Tt = 0 if tail_k is None else tail_k.shape[2]
         cap = max(tail_capacity or 0, 2 * (block_size or T), Tt)
         c = cls(H, D, block_size=block_size or T, k_rank_keys=kK, k_rank_values=kV, device=codes_k.device,
-                batch_size=B, max_blocks=max(NB, 1), tail_capacity=cap,
+                batch_size=B, max_blocks=max(NB, 1, max_blocks or 0), tail_capacity=cap,
                 quant_granularity="per_row" if per_row else "per_head", seed=seed)
         if NB:
             c.codes_k[:, :, :NB, :, :kK] = codes_k
