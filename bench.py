@@ -159,8 +159,9 @@ def rope_tables(torch, length, device, theta=1e6):
     return emb.cos().half().contiguous(), emb.sin().half().contiguous()
 
 
-def decode_args(lib_mod, cache, Q, out, cos, sin, qpos):
+def decode_args(lib_mod, cache, Q, out, cos, sin, qpos, split=0):
     a = lib_mod.ScDecodeArgs()
+    a.split = split
     tier = cache._tier()
     a.tier = ctypes.pointer(tier)
     a.q_heads, a.rope_mode = HQ, lib_mod.SC_ROPE_ABSOLUTE
@@ -265,14 +266,14 @@ def cpu_rsvd_baseline(M_gpu, omega):
                       f"per-row quantise, 8x512x128, k=16; best of 5 ({best * 1e3:.2f} ms)"}
 
 
-def time_decode(torch, lib, hip, caches, Q, cos, sin, qpos, warmup, steps):
+def time_decode(torch, lib, hip, caches, Q, cos, sin, qpos, warmup, steps, split=0):
     """Warm-up calls, then `steps` calls bracketed by HIP events on the launch
     stream; the tier sets in `caches` are used in rotation.  Returns
     (ms of the whole timed loop, sorted per-call ms)."""
     from unsloth_spectral import _lib
     b = Q.shape[0]
     outs = [torch.empty(b, HQ, D, dtype=torch.float16, device=Q.device) for _ in caches]
-    built = [decode_args(_lib, c, Q, o, cos, sin, qpos) for c, o in zip(caches, outs)]
+    built = [decode_args(_lib, c, Q, o, cos, sin, qpos, split) for c, o in zip(caches, outs)]
     nbytes = ctypes.c_size_t(0)
     _lib.check(lib.sc_decode_workspace_size(ctypes.byref(built[0][0]), ctypes.byref(nbytes)))
     ws = torch.empty(nbytes.value, dtype=torch.uint8, device=Q.device)
@@ -555,6 +556,8 @@ def main():
                     help="time only the batch-8 decode workload and the rSVD (profiling runs)")
     ap.add_argument("--model-loop", action="store_true",
                     help="run the Mistral-7B-shaped model loop instead and print its JSON line")
+    ap.add_argument("--split", type=int, default=0,
+                    help="workgroups per cold block for the batch-8 workload (0 = library's choice)")
     ap.add_argument("--prompt", type=int, default=8192)
     ap.add_argument("--decode-steps", type=int, default=256)
     ap.add_argument("--copy-probe-mib", type=int, default=0,
@@ -591,7 +594,8 @@ def main():
     g = torch.Generator(device=device)
     g.manual_seed(1)
     Q = torch.randn(B, HQ, D, generator=g, device=device).half()
-    total_ms, per_call = time_decode(torch, lib, hip, caches, Q, cos, sin, CTX - 1, args.warmup, args.steps)
+    total_ms, per_call = time_decode(torch, lib, hip, caches, Q, cos, sin, CTX - 1, args.warmup, args.steps,
+                                     args.split)
     avg_call_ms = sum(per_call) / len(per_call)
     med_call_ms = per_call[len(per_call) // 2]
     ms_per_step = total_ms / args.steps
