@@ -135,7 +135,7 @@ struct Lds {
   float* Ys;     // [kMaxRows][RM]  Y / Q rows, later Vh [RM][cols]
   float* Zs;     // [128][RM]       Z / Bp^T
   double* Gs;    // [RM][RM]
-  double* Ws;    // [RM][RM]        R^-1, then eigenvectors
+  double* Ws;    // [RM][RM]        eigenvectors
   float* Wf;     // [RM][RM]        W[:, ord] * S for the coefficient product
   double* red;   // [128]
   int* ord;      // [RM]
@@ -293,31 +293,70 @@ __device__ __forceinline__ void gemm_rows_mfma(const Job& j, int rows, int cols,
   }
 }
 
-// Zs[cols][RM] = M^T Ys; wave w owns d tiles w*DT .. w*DT+DT-1 (cols/16/4
-// each).  The M^T operand is gathered with 2-byte loads (8 rows of one
-// column per lane), prefetched one K step ahead.
+typedef short short4_t __attribute__((ext_vector_type(4)));
+constexpr int kColTile = 32;  // rows of M staged per step of gemm_cols_mfma
+
+// fp16 elements of gemm_cols_mfma's staging tile: 32 rows, padded by 8
+// elements (16 bytes) so the transposing reads of 4 consecutive rows fall
+// in distinct banks.
+__host__ __device__ constexpr int col_stage_elems(int cols) { return kColTile * (cols + 8); }
+
+// Zs[cols][RM] = M^T Ys for fp16 M.  M's rows are staged 32 at a time in
+// LDS (`stage`, row-major) with 16-byte loads; the next 32 rows are held in
+// registers while the current ones are consumed.  Lane (g, n)'s A operand
+// is rows 8g .. 8g+7 of column 16 d + n, read by two ds_read_b64_tr_b16:
+// that read gives lane j of a 16-lane group element j & 3 of the 4-element
+// chunk addressed by lane 4e + (j >> 2), so lane L addresses row
+// 8g + (L >> 2) (+4), columns 16 d + 4 (L & 3) .. +3.  Wave w owns d tiles
+// w*DT .. w*DT+DT-1 (cols/16/4 each).
 template <int RM>
-__device__ __forceinline__ void gemm_cols_mfma(const Job& j, int rows, int cols, const float* Ys, float* Zs) {
+__device__ __forceinline__ void gemm_cols_mfma(const Job& j, int rows, int cols, const float* Ys, float* Zs,
+                                               h16* stage) {
   constexpr int CT = (RM + 15) / 16;
-  const int lane = threadIdx.x & 63, g = lane >> 4, n = lane & 15, w = threadIdx.x >> 6;
+  static_assert(2 * RM * RM * sizeof(double) >= col_stage_elems(128) * sizeof(h16),
+                "the staging tile fits the Gs + Ws region, which is dead while this runs");
+  const int t = threadIdx.x, lane = t & 63, g = lane >> 4, n = lane & 15, w = t >> 6;
   const int DT = cols / 64;  // d tiles per wave: 2 (cols 128) or 1 (cols 64)
+  const int pitch = cols + 8;
+  const int cpr = cols / 8;  // 16-byte chunks per row
+  const int nchunks = kColTile * cpr;  // 512 or 256: one or two per thread
   float4_t acc[2][CT];
 #pragma unroll
   for (int dt = 0; dt < 2; ++dt)
 #pragma unroll
     for (int ct = 0; ct < CT; ++ct) acc[dt][ct] = (float4_t)0.f;
-  auto gather = [&](int k0, half8_t (&a)[2]) __attribute__((always_inline)) {
-#pragma unroll
-    for (int e = 0; e < 8; ++e) {
-      const h16* rp = reinterpret_cast<const h16*>(row_ptr(j, k0 + 8 * g + e, cols));
-#pragma unroll
-      for (int dt = 0; dt < 2; ++dt) a[dt][e] = dt < DT ? rp[(w * DT + dt) * 16 + n] : (h16)0;
-    }
+  // this thread's chunks t and t + kThreads of a tile: row c / cpr, 16-byte chunk c % cpr
+  const int c0 = t, c1 = t + kThreads;
+  const bool has1 = c1 < nchunks;
+  uint4 nx0, nx1;
+  auto fetch = [&](int k0) __attribute__((always_inline)) {
+    nx0 = *reinterpret_cast<const uint4*>(row_ptr(j, k0 + c0 / cpr, cols) + (c0 % cpr) * 16);
+    if (has1) nx1 = *reinterpret_cast<const uint4*>(row_ptr(j, k0 + c1 / cpr, cols) + (c1 % cpr) * 16);
   };
-  half8_t a[2], an[2];
-  gather(0, a);
-  for (int k0 = 0; k0 < rows; k0 += 32) {
-    if (k0 + 32 < rows) gather(k0 + 32, an);
+  auto put = [&]() __attribute__((always_inline)) {
+    *reinterpret_cast<uint4*>(stage + (c0 / cpr) * pitch + (c0 % cpr) * 8) = nx0;
+    if (has1) *reinterpret_cast<uint4*>(stage + (c1 / cpr) * pitch + (c1 % cpr) * 8) = nx1;
+  };
+  fetch(0);
+  put();
+  __syncthreads();
+  for (int k0 = 0; k0 < rows; k0 += kColTile) {
+    const bool more = k0 + kColTile < rows;
+    if (more) fetch(k0 + kColTile);
+    half8_t a[2];
+#pragma unroll
+    for (int dt = 0; dt < 2; ++dt) {
+      if (dt < DT) {
+        const h16* p0 = stage + (8 * g + (n >> 2)) * pitch + (w * DT + dt) * 16 + 4 * (n & 3);
+        typedef __attribute__((address_space(3))) short4_t lds_s4;
+        const short4_t lo = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_s4*)(p0));
+        const short4_t hi = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_s4*)(p0 + 4 * pitch));
+        const half4_t l4 = __builtin_bit_cast(half4_t, lo), h4 = __builtin_bit_cast(half4_t, hi);
+        a[dt] = (half8_t){l4.x, l4.y, l4.z, l4.w, h4.x, h4.y, h4.z, h4.w};
+      } else {
+        a[dt] = (half8_t)(h16)0;
+      }
+    }
 #pragma unroll
     for (int ct = 0; ct < CT; ++ct) {
       const int c = 16 * ct + n;
@@ -337,8 +376,11 @@ __device__ __forceinline__ void gemm_cols_mfma(const Job& j, int rows, int cols,
           acc[dt][ct] = __builtin_amdgcn_mfma_f32_16x16x32_f16(a[dt], bl, acc[dt][ct], 0, 0, 0);
         }
     }
-    a[0] = an[0];
-    a[1] = an[1];
+    __syncthreads();  // every wave is done with this tile
+    if (more) {
+      put();
+      __syncthreads();
+    }
   }
 #pragma unroll
   for (int dt = 0; dt < 2; ++dt)
@@ -352,7 +394,8 @@ __device__ __forceinline__ void gemm_cols_mfma(const Job& j, int rows, int cols,
       }
 }
 
-// Gs[c1][c2] = sum_row S[row][c1] S[row][c2] (c1, c2 < r) in fp64 on MFMA.
+// Gs[c1][c2] = sum_row S[row][c1] S[row][c2] (c1, c2 < r) in fp64 on MFMA
+// (nrows a multiple of 16).
 // Tile (ta, tb), ta <= tb, of the CT x CT upper triangle goes to wave
 // (tile index) % 4; the f64 16x16x4 output holds D[4 e + g][n] in lane
 // (g, n), element e.
@@ -365,12 +408,22 @@ __device__ __forceinline__ void gram_mfma(const float* S, int nrows, int r, doub
     for (int tb = ta; tb < CT; ++tb, ++tix) {
       if (tix % (kThreads / 64) != w) continue;
       const int ca = 16 * ta + n, cb = 16 * tb + n;
-      double4_t acc = {0.0, 0.0, 0.0, 0.0};
-      for (int k0 = 0; k0 < nrows; k0 += 4) {
-        const double av = ca < RM ? (double)S[(k0 + g) * RM + ca] : 0.0;
-        const double bv = cb < RM ? (double)S[(k0 + g) * RM + cb] : 0.0;
-        acc = __builtin_amdgcn_mfma_f64_16x16x4f64(av, bv, acc, 0, 0, 0);
+      // four independent accumulation chains (rows k0 + 4u + g), summed in
+      // a fixed order at the end
+      double4_t acc = {0.0, 0.0, 0.0, 0.0}, acc1 = acc, acc2 = acc, acc3 = acc;
+      for (int k0 = 0; k0 < nrows; k0 += 16) {
+        double av[4], bv[4];
+#pragma unroll
+        for (int u = 0; u < 4; ++u) {
+          av[u] = ca < RM ? (double)S[(k0 + 4 * u + g) * RM + ca] : 0.0;
+          bv[u] = cb < RM ? (double)S[(k0 + 4 * u + g) * RM + cb] : 0.0;
+        }
+        acc = __builtin_amdgcn_mfma_f64_16x16x4f64(av[0], bv[0], acc, 0, 0, 0);
+        acc1 = __builtin_amdgcn_mfma_f64_16x16x4f64(av[1], bv[1], acc1, 0, 0, 0);
+        acc2 = __builtin_amdgcn_mfma_f64_16x16x4f64(av[2], bv[2], acc2, 0, 0, 0);
+        acc3 = __builtin_amdgcn_mfma_f64_16x16x4f64(av[3], bv[3], acc3, 0, 0, 0);
       }
+      acc = (acc + acc1) + (acc2 + acc3);
 #pragma unroll
       for (int e = 0; e < 4; ++e) {
         const int c1 = 16 * ta + 4 * e + g, c2 = 16 * tb + n;
@@ -380,6 +433,79 @@ __device__ __forceinline__ void gram_mfma(const float* S, int nrows, int r, doub
         }
       }
     }
+}
+
+// Gs = S^T S (c1, c2 < r) over nrows rows of S [nrows][RM] (nrows a multiple
+// of 32) in fp64 on MFMA, the rows split over the four waves: wave w takes
+// rows [w, w+1) * nrows / 4 and every upper-triangular 16x16 tile, with two
+// accumulators per tile (alternate 4-row steps).  The partial sums meet in
+// `slab` (2 * NT * 256 doubles, NT tiles) in a fixed order:
+// (w0 + w2) + (w1 + w3).
+template <int RM>
+__device__ __forceinline__ void gram_rows_mfma(const float* S, int nrows, int r, double* Gs, double* slab) {
+  constexpr int CT = (RM + 15) / 16;
+  constexpr int NT = CT * (CT + 1) / 2;
+  static_assert(kThreads == 256, "four waves");
+  static_assert(2 * NT * 256 * sizeof(double) <= sizeof(float) * (128 * RM + RM * RM),
+                "the two slabs fit the Zs + Wf region");
+  const int lane = threadIdx.x & 63, g = lane >> 4, n = lane & 15, w = threadIdx.x >> 6;
+  double4_t acc[2][NT];
+#pragma unroll
+  for (int u = 0; u < 2; ++u)
+#pragma unroll
+    for (int ti = 0; ti < NT; ++ti) acc[u][ti] = (double4_t){0.0, 0.0, 0.0, 0.0};
+  const int rpw = nrows / 4;
+  for (int k0 = w * rpw; k0 < (w + 1) * rpw; k0 += 8) {
+    double v[2][CT];
+#pragma unroll
+    for (int u = 0; u < 2; ++u)
+#pragma unroll
+      for (int ct = 0; ct < CT; ++ct)
+        v[u][ct] = 16 * ct + n < RM ? (double)S[(k0 + 4 * u + g) * RM + 16 * ct + n] : 0.0;
+#pragma unroll
+    for (int u = 0; u < 2; ++u) {
+      int ti = 0;
+#pragma unroll
+      for (int ta = 0; ta < CT; ++ta)
+#pragma unroll
+        for (int tb = ta; tb < CT; ++tb, ++ti)
+          acc[u][ti] = __builtin_amdgcn_mfma_f64_16x16x4f64(v[u][ta], v[u][tb], acc[u][ti], 0, 0, 0);
+    }
+  }
+#pragma unroll
+  for (int ti = 0; ti < NT; ++ti) acc[0][ti] = acc[0][ti] + acc[1][ti];
+  auto slab_at = [&](int sb, int ti) __attribute__((always_inline)) {
+    return reinterpret_cast<double4_t*>(slab + ((sb * NT + ti) * 64 + lane) * 4);
+  };
+  if (w >= 2)
+#pragma unroll
+    for (int ti = 0; ti < NT; ++ti) *slab_at(w - 2, ti) = acc[0][ti];
+  __syncthreads();
+  if (w < 2)
+#pragma unroll
+    for (int ti = 0; ti < NT; ++ti) acc[0][ti] = acc[0][ti] + *slab_at(w, ti);
+  __syncthreads();
+  if (w == 1)
+#pragma unroll
+    for (int ti = 0; ti < NT; ++ti) *slab_at(0, ti) = acc[0][ti];
+  __syncthreads();
+  if (w == 0) {
+    int ti = 0;
+#pragma unroll
+    for (int ta = 0; ta < CT; ++ta)
+#pragma unroll
+      for (int tb = ta; tb < CT; ++tb, ++ti) {
+        const double4_t sum = acc[0][ti] + *slab_at(0, ti);
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+          const int c1 = 16 * ta + 4 * e + g, c2 = 16 * tb + n;
+          if (c1 < r && c2 < r) {
+            Gs[c1 * RM + c2] = sum[e];
+            Gs[c2 * RM + c1] = sum[e];
+          }
+        }
+      }
+  }
 }
 
 // Orders the LDS writes of a wave before its later LDS reads by other lanes.
@@ -401,160 +527,258 @@ __device__ __forceinline__ double rsqrt64(double x) {
   return y * fma(-0.5 * x * y, y, 1.5);
 }
 
-// Cholesky G = L L^T of Gs (r x r, r <= RM) by wave 0: lane i keeps row i
-// in registers, the steps are unrolled (register indices are static) and
-// column jc is broadcast through LDS (col).  Writes R = L^T into Ws
-// (upper triangle, row-major) and 1/R[c][c] (0 for dead columns, whose
-// pivot vanished) into rdiag.
+// Wave-uniform copy of lane `src`'s double (src a compile-time or uniform index).
+__device__ __forceinline__ double lane_bcast(double v, int src) {
+  const long long u = __double_as_longlong(v);
+  const int lo = __builtin_amdgcn_readlane((int)(u & 0xffffffffLL), src);
+  const int hi = __builtin_amdgcn_readlane((int)(u >> 32), src);
+  return __longlong_as_double(((long long)hi << 32) | (unsigned)lo);
+}
+
+// Cholesky G = L L^T of Gs (r x r, r <= RM) and X = R^{-1} with R = L^T, by
+// wave 0.  Lane i keeps row i of L in registers; the steps are unrolled, so
+// register indices are static, and values move between lanes by readlane
+// (no LDS, no barrier inside).  Dead columns (pivot <= 1e-26 of the largest
+// diagonal entry) get L[:, j] = 0 and X[:, j] = 0.  Then lane i forms row i
+// of L^{-1} by forward substitution against the rows of the lanes before it,
+// and writes it as column i of X (fp32, row-major [RM][RM], upper
+// triangular) into Xf.
 template <int RM>
-__device__ __forceinline__ void cholesky_wave(const double* Gs, double* Ws, double* rdiag, double* col, int r) {
+__device__ __forceinline__ void cholesky_inv_wave(const double* Gs, float* Xf, int r) {
   if (threadIdx.x < 64) {
     const int lane = threadIdx.x;
     const bool act = lane < r;
     double row[RM];
 #pragma unroll
     for (int k = 0; k < RM; ++k) row[k] = (act && k < r) ? Gs[lane * RM + k] : 0.0;
-    double gm = act ? row[0] : 0.0;
+    double gm = 0.0;
 #pragma unroll
-    for (int k = 1; k < RM; ++k)
-      if (k == lane) gm = row[k];
-#pragma unroll
-    for (int o = 32; o > 0; o >>= 1) gm = fmax(gm, __shfl_xor(gm, o));
+    for (int k = 0; k < RM; ++k) gm = fmax(gm, lane_bcast(row[k], k));
     const double tol = gm * 1e-26 + 1e-300;
+    double il_own = 0.0;  // 1 / L[lane][lane] (0 when dead)
 #pragma unroll
     for (int jc = 0; jc < RM; ++jc) {
       if (jc < r) {  // wave-uniform
-        const double piv = __shfl(row[jc], jc);
+        const double piv = lane_bcast(row[jc], jc);
         const bool dead = !(piv > tol);
         const double il = dead ? 0.0 : rsqrt64(piv);
-        if (lane > jc) row[jc] *= il;  // L[lane][jc]
-        if (lane == jc) row[jc] = dead ? 0.0 : piv * il;  // L[jc][jc] = sqrt(piv)
-        col[lane] = row[jc];
-        wave_sync();
+        if (lane > jc) row[jc] *= il;                     // L[lane][jc]
+        if (lane == jc) {
+          row[jc] = dead ? 0.0 : piv * il;                // L[jc][jc] = sqrt(piv)
+          il_own = il;
+        }
 #pragma unroll
-        for (int k = jc + 1; k < RM; ++k)
-          if (lane > jc && k <= lane) row[k] -= row[jc] * col[k];
-        if (lane == 0) rdiag[jc] = il;
-        wave_sync();
+        for (int k = jc + 1; k < RM; ++k) {
+          const double lk = lane_bcast(row[jc], k);       // L[k][jc]
+          if (lane > jc) row[k] = fma(-row[jc], lk, row[k]);
+        }
       }
     }
-    // R[k][lane] = L[lane][k] for k <= lane
+    // y = row `lane` of L^{-1}: y[n] = (delta(lane, n) - sum_{m<lane} L[lane][m] Y[m][n]) / L[lane][lane]
+    double y[RM];
 #pragma unroll
-    for (int k = 0; k < RM; ++k)
-      if (act && k <= lane) Ws[k * RM + lane] = row[k];
+    for (int n = 0; n < RM; ++n) y[n] = 0.0;
+#pragma unroll
+    for (int m = 0; m < RM; ++m) {
+      if (lane == m) {
+#pragma unroll
+        for (int n = 0; n <= m; ++n) y[n] = ((n == m ? 1.0 : 0.0) - y[n]) * il_own;
+      }
+      const double lim = row[m];  // L[lane][m]
+#pragma unroll
+      for (int n = 0; n <= m; ++n) {
+        const double ymn = lane_bcast(y[n], m);
+        if (lane > m) y[n] = fma(lim, ymn, y[n]);
+      }
+    }
+    // X[n][lane] = Y[lane][n]
+    if (lane < RM) {
+#pragma unroll
+      for (int n = 0; n < RM; ++n) Xf[n * RM + lane] = (act && n <= lane) ? (float)y[n] : 0.f;
+    }
   }
   __syncthreads();
 }
 
-// Rows of Ys <- rows R^{-1} by forward substitution (q R = y, R upper
-// triangular in Ws, reciprocal diagonal in rdiag; dead columns give 0), in
-// fp64, one row at a time per thread.
+// Rows of Ys <- rows of Ys X (X upper triangular, fp32 in Xf).  Thread t
+// takes rows t and t + kThreads together (kept in registers), so each
+// float4 of X read from LDS (a broadcast) serves both.  Output columns go
+// four at a time in a runtime loop, which bounds the loads in flight; no
+// dependency chain across columns.
 template <int RM>
-__device__ __forceinline__ void solve_rows(float* Ys, int rows, const double* Ws, const double* rdiag, int r) {
-  for (int row = threadIdx.x; row < rows; row += kThreads) {
-    double q[RM];
+__device__ __forceinline__ void apply_rinv(float* Ys, int rows, const float* Xf) {
+  static_assert(RM % 4 == 0 && kMaxRows <= 2 * kThreads, "two rows per thread, float4 columns");
+  const int t = threadIdx.x;
+  const bool va = t < rows, vb = t + kThreads < rows;
+  float ya[RM], yb[RM];
 #pragma unroll
-    for (int c = 0; c < RM; ++c) {
-      double a = Ys[row * RM + c];
+  for (int c = 0; c < RM; c += 4) {
+    const float4 a4 = va ? *reinterpret_cast<const float4*>(Ys + t * RM + c) : make_float4(0.f, 0.f, 0.f, 0.f);
+    const float4 b4 = vb ? *reinterpret_cast<const float4*>(Ys + (t + kThreads) * RM + c) : make_float4(0.f, 0.f, 0.f, 0.f);
+    ya[c] = a4.x; ya[c + 1] = a4.y; ya[c + 2] = a4.z; ya[c + 3] = a4.w;
+    yb[c] = b4.x; yb[c + 1] = b4.y; yb[c + 2] = b4.z; yb[c + 3] = b4.w;
+  }
+#pragma unroll 1
+  for (int c = 0; c < RM; c += 4) {
+    float4 qa = make_float4(0.f, 0.f, 0.f, 0.f), qb = qa;
 #pragma unroll
-      for (int i = 0; i < c; ++i) a = fma(-q[i], Ws[i * RM + c], a);
-      q[c] = c < r ? a * rdiag[c] : 0.0;
+    for (int m = 0; m < RM; ++m) {
+      if (m < c + 4) {  // X[m][c..c+3] = 0 below the diagonal
+        const float4 x4 = *reinterpret_cast<const float4*>(Xf + m * RM + c);
+        qa.x = fmaf(ya[m], x4.x, qa.x);
+        qa.y = fmaf(ya[m], x4.y, qa.y);
+        qa.z = fmaf(ya[m], x4.z, qa.z);
+        qa.w = fmaf(ya[m], x4.w, qa.w);
+        qb.x = fmaf(yb[m], x4.x, qb.x);
+        qb.y = fmaf(yb[m], x4.y, qb.y);
+        qb.z = fmaf(yb[m], x4.z, qb.z);
+        qb.w = fmaf(yb[m], x4.w, qb.w);
+      }
     }
-#pragma unroll
-    for (int c = 0; c < RM; ++c) Ys[row * RM + c] = (float)q[c];
+    if (va) *reinterpret_cast<float4*>(Ys + t * RM + c) = qa;
+    if (vb) *reinterpret_cast<float4*>(Ys + (t + kThreads) * RM + c) = qb;
   }
 }
 
-// Cyclic parallel Jacobi on the symmetric Gs by wave 0: Gs -> diagonal,
-// Ws = eigenvectors.  The round-robin pairing runs over RM players (RM
-// even); rows and columns >= r are zeroed first, so their rotations are the
-// identity.  Loop shapes are compile-time (RM) so index arithmetic is
-// cheap; rotation parameters use the hardware reciprocal / rsqrt refined by
-// Newton steps; rows, then columns, are updated lane-parallel.
+// Players p < q of round-robin pair m at `step` (P players, P even; pair m
+// is slots m and P-1-m of a circle whose player 0 stays put).
+__device__ __forceinline__ void jacobi_players(int P, int m, int step, int& pp, int& qq) {
+  const int i1 = m, i2 = P - 1 - m;
+  const int a = i1 == 0 ? 0 : 1 + (i1 - 1 + step) % (P - 1);
+  const int b = 1 + (i2 - 1 + step) % (P - 1);
+  pp = a < b ? a : b;
+  qq = a < b ? b : a;
+}
+
+// Jacobi rotation (c, s) that zeroes G[p][q]: tau in fp64 (scale-free), the
+// angle in fp32, then (c, s) renormalised in fp64 by one Newton step, so
+// c^2 + s^2 = 1 to ~1e-14.  An fp32 angle leaves ~1e-7 of G[p][q] behind,
+// which the next sweep removes.
+__device__ __forceinline__ void jacobi_rotation(double app, double aqq, double apq, double& c, double& sn) {
+  c = 1.0;
+  sn = 0.0;
+  if (apq != 0.0) {
+    const float tau = (float)((aqq - app) * rcp64(2.0 * apq));
+    const float at = fabsf(tau);
+    const float tt = at > 1e18f ? __builtin_amdgcn_rcpf(2.0f * tau)
+                                : copysignf(__builtin_amdgcn_rcpf(at + __builtin_amdgcn_sqrtf(fmaf(tau, tau, 1.0f))), tau);
+    const float c32 = __builtin_amdgcn_rsqf(fmaf(tt, tt, 1.0f));
+    const double cd = (double)c32, sd = (double)(tt * c32);
+    const double f = fma(-0.5, fma(cd, cd, sd * sd), 1.5);
+    c = cd * f;
+    sn = sd * f;
+  }
+}
+
+// Cyclic parallel Jacobi on the symmetric Gs by the whole workgroup:
+// Gs -> diagonal, Ws = eigenvectors.  The round-robin pairing runs over the
+// P = r rounded up to even players (P - 1 rounds per sweep); rows and
+// columns >= r are zeroed first, so a padded player's rotations are the
+// identity.  One round is two barrier-separated phases:
+//   1. NP = P/2 threads compute the rotation (c, s) of one pair each;
+//   2. thread i < NB rotates the 2x2 block (pair mi, pair mk), mi <= mk, of
+//      Gs from both sides (Gs <- J^T Gs J) and writes its mirror; thread t
+//      rotates rows t / NP, t / NP + cnt, ... of pair t % NP of Ws from the
+//      right (cnt = number of threads with that pair).  Pair players are
+//      recomputed arithmetically, so the rotation and element reads go out
+//      together; each element has one owner, so the updates are in place.
+// Stops when the off-diagonal mass is <= 1e-24 of the diagonal mass.
+// scratch: >= 2 * RM / 2 + 2 * kThreads / 64 doubles.
 template <int RM>
-__device__ __forceinline__ void jacobi_eig_wave(double* Gs, double* Ws, double* rot, int r) {
+__device__ __forceinline__ void jacobi_eig(double* Gs, double* Ws, double* scratch, int r) {
   static_assert(RM % 2 == 0, "even player count");
   constexpr int NP = RM / 2;
-  if (threadIdx.x < 64) {
-    const int lane = threadIdx.x;
-    for (int e = lane; e < RM * RM; e += 64) {
-      const int i = e / RM, k = e % RM;
-      Ws[e] = (i == k) ? 1.0 : 0.0;
-      if (i >= r || k >= r) Gs[e] = 0.0;
+  constexpr int NB = NP * (NP + 1) / 2;  // upper-triangular 2x2 blocks
+  constexpr int NW = kThreads / 64;
+  static_assert(NB <= kThreads && 2 * NP + 2 * NW <= 128, "one block per thread; scratch holds 128 doubles");
+  const int t = threadIdx.x;
+  const int P = r + (r & 1), NPr = P / 2, NBr = NPr * (NPr + 1) / 2;
+  double* rot = scratch;            // [NP][2] = (c, s)
+  double* part = scratch + 2 * NP;  // [NW][2] partial sums
+  for (int e = t; e < RM * RM; e += kThreads) {
+    const int i = e / RM, k = e % RM;
+    Ws[e] = (i == k) ? 1.0 : 0.0;
+    if (i >= r || k >= r) Gs[e] = 0.0;
+  }
+  int mi = 0, mk = 0;
+  if (t < NBr) {
+    mk = (int)((sqrtf(8.0f * (float)t + 1.0f) - 1.0f) * 0.5f);  // t = mk (mk + 1) / 2 + mi
+    if ((mk + 1) * (mk + 2) / 2 <= t) ++mk;
+    if (mk * (mk + 1) / 2 > t) --mk;
+    mi = t - mk * (mk + 1) / 2;
+  }
+  const int mv = t % NPr, vcnt = (kThreads - mv + NPr - 1) / NPr;
+  __syncthreads();
+  for (int sweep = 0; sweep < 30; ++sweep) {
+    double off = 0.0, dia = 0.0;
+    for (int e = t; e < RM * RM; e += kThreads) {
+      const double v = Gs[e];
+      if (e / RM == e % RM)
+        dia += v * v;
+      else
+        off += v * v;
     }
-    int* pq = reinterpret_cast<int*>(rot + 2 * NP);
-    wave_sync();
-    for (int sweep = 0; sweep < 30; ++sweep) {
-      double off = 0.0, dia = 0.0;
-      for (int e = lane; e < RM * RM; e += 64) {
-        const double v = Gs[e];
-        if (e / RM == e % RM)
-          dia += v * v;
-        else
-          off += v * v;
-      }
 #pragma unroll
-      for (int o = 32; o > 0; o >>= 1) {
-        off += __shfl_xor(off, o);
-        dia += __shfl_xor(dia, o);
-      }
-      if (off <= 1e-24 * dia || dia == 0.0) break;  // off-diagonal below 1e-12 of the diagonal
-      for (int step = 0; step < RM - 1; ++step) {
-        if (lane < NP) {
-          const int i1 = lane, i2 = RM - 1 - lane;
-          int pp = i1 == 0 ? 0 : 1 + (i1 - 1 + step) % (RM - 1);
-          int qq = 1 + (i2 - 1 + step) % (RM - 1);
-          if (pp > qq) {
-            const int tmp = pp;
-            pp = qq;
-            qq = tmp;
-          }
-          const double apq = Gs[pp * RM + qq], app = Gs[pp * RM + pp], aqq = Gs[qq * RM + qq];
-          double c = 1.0, sn = 0.0;
-          if (apq != 0.0) {
-            const double tau = (aqq - app) * rcp64(2.0 * apq);
-            const double tt = (tau >= 0.0 ? 1.0 : -1.0) * rcp64(fabs(tau) + sqrt(1.0 + tau * tau));
-            c = rsqrt64(1.0 + tt * tt);
-            sn = tt * c;
-          }
-          rot[2 * lane] = c;
-          rot[2 * lane + 1] = sn;
-          pq[2 * lane] = pp;
-          pq[2 * lane + 1] = qq;
-        }
-        wave_sync();
-        // rows: A <- J^T A ; element (pair pi, column k)
+    for (int o = 32; o > 0; o >>= 1) {
+      off += __shfl_xor(off, o);
+      dia += __shfl_xor(dia, o);
+    }
+    if ((t & 63) == 0) {
+      part[2 * (t >> 6)] = off;
+      part[2 * (t >> 6) + 1] = dia;
+    }
+    __syncthreads();
+    off = 0.0;
+    dia = 0.0;
 #pragma unroll
-        for (int e0 = 0; e0 < NP * RM; e0 += 64) {
-          const int e = e0 + lane;
-          if (e < NP * RM) {
-            const int pi = e / RM, k = e % RM;
-            const double c = rot[2 * pi], sn = rot[2 * pi + 1];
-            const int pp = pq[2 * pi], qq = pq[2 * pi + 1];
-            const double ap = Gs[pp * RM + k], aq = Gs[qq * RM + k];
-            Gs[pp * RM + k] = c * ap - sn * aq;
-            Gs[qq * RM + k] = sn * ap + c * aq;
-          }
-        }
-        wave_sync();
-        // columns: A <- A J, V <- V J
-#pragma unroll
-        for (int e0 = 0; e0 < NP * RM; e0 += 64) {
-          const int e = e0 + lane;
-          if (e < NP * RM) {
-            const int pi = e / RM, k = e % RM;
-            const double c = rot[2 * pi], sn = rot[2 * pi + 1];
-            const int pp = pq[2 * pi], qq = pq[2 * pi + 1];
-            const double ap = Gs[k * RM + pp], aq = Gs[k * RM + qq];
-            Gs[k * RM + pp] = c * ap - sn * aq;
-            Gs[k * RM + qq] = sn * ap + c * aq;
-            const double vp = Ws[k * RM + pp], vq = Ws[k * RM + qq];
-            Ws[k * RM + pp] = c * vp - sn * vq;
-            Ws[k * RM + qq] = sn * vp + c * vq;
-          }
-        }
-        wave_sync();
+    for (int w = 0; w < NW; ++w) {  // same order in every thread: a uniform decision
+      off += part[2 * w];
+      dia += part[2 * w + 1];
+    }
+    if (off <= 1e-24 * dia || dia == 0.0) break;  // off-diagonal norm below 1e-12 of the diagonal
+    for (int step = 0; step < P - 1; ++step) {
+      if (t < NPr) {
+        int pp, qq;
+        jacobi_players(P, t, step, pp, qq);
+        double c, sn;
+        jacobi_rotation(Gs[pp * RM + pp], Gs[qq * RM + qq], Gs[pp * RM + qq], c, sn);
+        rot[2 * t] = c;
+        rot[2 * t + 1] = sn;
       }
+      __syncthreads();
+      if (t < NBr) {
+        int pi, qi, pk, qk;
+        jacobi_players(P, mi, step, pi, qi);
+        jacobi_players(P, mk, step, pk, qk);
+        const double ci = rot[2 * mi], si = rot[2 * mi + 1], ck = rot[2 * mk], sk = rot[2 * mk + 1];
+        const double a00 = Gs[pi * RM + pk], a01 = Gs[pi * RM + qk];
+        const double a10 = Gs[qi * RM + pk], a11 = Gs[qi * RM + qk];
+        const double b00 = ci * a00 - si * a10, b01 = ci * a01 - si * a11;  // rows: J^T A
+        const double b10 = si * a00 + ci * a10, b11 = si * a01 + ci * a11;
+        const double n00 = ck * b00 - sk * b01, n01 = sk * b00 + ck * b01;  // columns: (J^T A) J
+        const double n10 = ck * b10 - sk * b11, n11 = sk * b10 + ck * b11;
+        Gs[pi * RM + pk] = n00;
+        Gs[pi * RM + qk] = n01;
+        Gs[qi * RM + pk] = n10;
+        Gs[qi * RM + qk] = n11;
+        if (mi != mk) {
+          Gs[pk * RM + pi] = n00;
+          Gs[qk * RM + pi] = n01;
+          Gs[pk * RM + qi] = n10;
+          Gs[qk * RM + qi] = n11;
+        }
+      }
+      {
+        int pm, qm;
+        jacobi_players(P, mv, step, pm, qm);
+        const double cm = rot[2 * mv], sm = rot[2 * mv + 1];
+        for (int c = t / NPr; c < P; c += vcnt) {
+          const double vp = Ws[c * RM + pm], vq = Ws[c * RM + qm];
+          Ws[c * RM + pm] = cm * vp - sm * vq;
+          Ws[c * RM + qm] = sm * vp + cm * vq;
+        }
+      }
+      __syncthreads();
     }
   }
   __syncthreads();
@@ -594,17 +818,17 @@ __device__ __forceinline__ void run_matrix(const RsvdParams& p, const Job& j, in
   };
   auto mul_mt = [&]() __attribute__((always_inline)) {  // Zs = M^T Ys
     if (mf)
-      gemm_cols_mfma<RM>(j, rows, cols, L.Ys, L.Zs);
+      gemm_cols_mfma<RM>(j, rows, cols, L.Ys, L.Zs, reinterpret_cast<h16*>(L.Gs));
     else
       gemm_cols<RM>(j, rows, cols, L.Ys, L.Zs);
   };
   auto orth_ys = [&](int passes) __attribute__((always_inline)) {  // Ys <- Q of Ys (CholeskyQR passes)
     for (int ps = 0; ps < passes; ++ps) {
       __syncthreads();
-      gram_mfma<RM>(L.Ys, rows, r, L.Gs);
+      gram_rows_mfma<RM>(L.Ys, rows, r, L.Gs, reinterpret_cast<double*>(L.Zs));  // Zs, Wf: dead here
       __syncthreads();
-      cholesky_wave<RM>(L.Gs, L.Ws, L.red, L.red + RM, r);
-      solve_rows<RM>(L.Ys, rows, L.Ws, L.red, r);
+      cholesky_inv_wave<RM>(L.Gs, L.Wf, r);
+      apply_rinv<RM>(L.Ys, rows, L.Wf);
     }
   };
   mul_m();
@@ -623,7 +847,7 @@ __device__ __forceinline__ void run_matrix(const RsvdParams& p, const Job& j, in
   __syncthreads();
   gram_mfma<RM>(L.Zs, cols, r, L.Gs);  // Bp Bp^T
   __syncthreads();
-  jacobi_eig_wave<RM>(L.Gs, L.Ws, L.red, r);
+  jacobi_eig<RM>(L.Gs, L.Ws, L.red, r);
   // ---- eigenvalues in descending order: lane c takes rank = #{larger, or equal with lower index}
   if (t < r) {
     const double lc = L.Gs[t * RM + t];
@@ -635,40 +859,67 @@ __device__ __forceinline__ void run_matrix(const RsvdParams& p, const Job& j, in
     L.ord[rank] = t;
   }
   __syncthreads();
-  // Wf[c][i] = W[c][ord_i] * S_i  (i < k)
-  for (int e = t; e < r * k; e += kThreads) {
-    const int c = e / k, i = e % k;
-    const int oi = L.ord[i];
-    const double sv = sqrt(fmax(L.Gs[oi * RM + oi], 0.0));
-    L.Wf[c * RM + i] = (float)(L.Ws[c * RM + oi] * sv);
+  // Wf[c][i] = W[c][ord_i] * S_i  (i < k; 0 for k <= i < RM)
+  for (int e = t; e < r * RM; e += kThreads) {
+    const int c = e / RM, i = e % RM;
+    float v = 0.f;
+    if (i < k) {
+      const int oi = L.ord[i];
+      v = (float)(L.Ws[c * RM + oi] * sqrt(fmax(L.Gs[oi * RM + oi], 0.0)));
+    }
+    L.Wf[e] = v;
   }
   __syncthreads();
-  // ---- coefficients of my rows (Q in Ys): coeff[i] = sum_c Q[row][c] Wf[c][i]
+  // ---- coefficients of my rows (Q in Ys): coeff[i] = sum_c Q[row][c] Wf[c][i];
+  // c runs in a runtime loop and Wf rows are read as float4 broadcasts
   const bool v0 = t < rows, v1 = t + kThreads < rows;
   float cf0[RM], cf1[RM];
 #pragma unroll
   for (int i = 0; i < RM; ++i) cf0[i] = cf1[i] = 0.f;
+#pragma unroll 1
+  for (int c = 0; c < r; ++c) {
+    const float q0 = v0 ? L.Ys[t * RM + c] : 0.f, q1 = v1 ? L.Ys[(t + kThreads) * RM + c] : 0.f;
 #pragma unroll
-  for (int c = 0; c < RM; ++c) {
-    if (c < r) {
-      const float q0 = v0 ? L.Ys[t * RM + c] : 0.f, q1 = v1 ? L.Ys[(t + kThreads) * RM + c] : 0.f;
-#pragma unroll
-      for (int i = 0; i < RM; ++i)
-        if (i < k) {
-          const float w = L.Wf[c * RM + i];
-          cf0[i] = fmaf(q0, w, cf0[i]);
-          cf1[i] = fmaf(q1, w, cf1[i]);
-        }
+    for (int i = 0; i < RM; i += 4) {
+      if (i < k) {
+        const float4 w = *reinterpret_cast<const float4*>(L.Wf + c * RM + i);
+        cf0[i] = fmaf(q0, w.x, cf0[i]);
+        cf0[i + 1] = fmaf(q0, w.y, cf0[i + 1]);
+        cf0[i + 2] = fmaf(q0, w.z, cf0[i + 2]);
+        cf0[i + 3] = fmaf(q0, w.w, cf0[i + 3]);
+        cf1[i] = fmaf(q1, w.x, cf1[i]);
+        cf1[i + 1] = fmaf(q1, w.y, cf1[i + 1]);
+        cf1[i + 2] = fmaf(q1, w.z, cf1[i + 2]);
+        cf1[i + 3] = fmaf(q1, w.w, cf1[i + 3]);
+      }
     }
   }
   __syncthreads();  // Q no longer needed: Ys is reused for Vh
-  // Vh (unnormalised) into Ys as [k][cols]: Vh_i[d] = sum_c W[c][ord_i] Bp^T[d][c]
-  for (int e = t; e < k * cols; e += kThreads) {
-    const int i = e / cols, d = e % cols;
-    const int oi = L.ord[i];
-    double acc = 0.0;
-    for (int c = 0; c < r; ++c) acc = fma(L.Ws[c * RM + oi], (double)L.Zs[d * RM + c], acc);
-    L.Ys[i * cols + d] = (float)acc;
+  // Vh (unnormalised) into Ys as [k][cols]: Vh_i[d] = sum_c W[c][ord_i] Bp^T[d][c].
+  // Thread t owns column d = t % cols (its Bp^T row in registers) and ranks
+  // t / cols, t / cols + kThreads / cols, ...; W reads are wave broadcasts.
+  {
+    const int d = t % cols, istep = kThreads / cols;
+    float z[RM];
+#pragma unroll
+    for (int c = 0; c < RM; c += 4) {
+      const float4 z4 = *reinterpret_cast<const float4*>(L.Zs + d * RM + c);
+      z[c] = z4.x;
+      z[c + 1] = z4.y;
+      z[c + 2] = z4.z;
+      z[c + 3] = z4.w;
+    }
+#pragma unroll 2
+    for (int i = t / cols; i < k; i += istep) {
+      const int oi = L.ord[i];
+      double a0 = 0.0, a1 = 0.0;
+#pragma unroll
+      for (int c = 0; c < RM; c += 2) {
+        if (c < r) a0 = fma(L.Ws[c * RM + oi], (double)z[c], a0);
+        if (c + 1 < r) a1 = fma(L.Ws[(c + 1) * RM + oi], (double)z[c + 1], a1);
+      }
+      L.Ys[i * cols + d] = (float)(a0 + a1);
+    }
   }
   __syncthreads();
   for (int i = t >> 6; i < k; i += kThreads / 64) {  // row norms -> 1/norm (0 for vanished rows), one wave per row
