@@ -34,6 +34,7 @@
 // rope_mode = none.
 #include <math.h>
 
+#include <atomic>
 #include <type_traits>
 
 #include "sc_common.h"
@@ -45,6 +46,11 @@ constexpr int kThreads = 64 * kWaves;
 constexpr int kTile = 16;
 constexpr int kMaxRep = 16;
 constexpr long kFillUnits = 512;  // two resident workgroups per CU on 256 CUs
+// A CU's wave arbiter favours its oldest waves: of two resident workgroups,
+// the one dispatched second runs at about half the speed of the first and
+// finishes ~8 us after it (batch 8, 16K context).  It raises its priority
+// once it has finished this many ranges, which evens out the finish times.
+constexpr int kYoungPrioRange = 2;
 constexpr int kVRow = 132;                              // LDS row (halves) of a staged V tile
 constexpr int kCombineWaves = 4;  // waves (query heads) per combine workgroup
 constexpr float kLog2e = 1.4426950408889634f;
@@ -53,6 +59,7 @@ struct DecodeParams {
   int B, Hq, Hkv, nrep, TB, NB, TCAP, per_row, rope_mode, rope_len, halves_equal;
   int grid_blocks, tpw, n_hq, cold_units, units_per_bh, fold_tail;
   int split;  // workgroups per cold block (each takes TB / (64 * split) consecutive ranges)
+  int young_slot;  // slots (blockIdx / 8) from here on were dispatched after every CU had a workgroup
   long n_cold_units;  // summed over (b, head group)
   float scale;
   const h16* q;
@@ -875,6 +882,7 @@ __device__ void cold_unit(const DecodeParams& p, int b, int hq, int j, char* sme
   const int lane = threadIdx.x & 63, g = lane >> 4, n = lane & 15;
   const int w = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);  // wave-uniform: per-head bases in SGPRs
   const int h = hq * kWaves + w;
+  const bool young = (int)(blockIdx.x >> 3) >= p.young_slot;
   // The branch-free path runs only when the KV heads fill whole groups of
   // four: with no idle wave, its loads are issued without branches.
   const bool hvalid = !GEN || h < p.Hkv;
@@ -1000,6 +1008,7 @@ __device__ void cold_unit(const DecodeParams& p, int b, int hq, int j, char* sme
       stage_store<D, HE, T>(next, smap, stage_fetch<D, HE, T>(p, smap, start + (r0 + rr + 1) * T, qp, dist));
     }
     __syncthreads();
+    if (young && rr == kYoungPrioRange) __builtin_amdgcn_s_setprio(2);
   };
   using TT = std::integral_constant<bool, true>;
   using FF = std::integral_constant<bool, false>;
@@ -1254,6 +1263,21 @@ int fill_params(const ScDecodeArgs* a, DecodeParams* p) {
   return SC_OK;
 }
 
+// Compute units per XCD of the current device (8 XCDs), cached per device.
+int cus_per_xcd() {
+  static std::atomic<int> cache[64];
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return 32;
+  int v = cache[dev].load(std::memory_order_relaxed);
+  if (v == 0) {
+    int n = 0;
+    if (hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || n < 8) n = 256;
+    v = n / 8;
+    cache[dev].store(v, std::memory_order_relaxed);
+  }
+  return v;
+}
+
 size_t workspace_bytes(const DecodeParams& p, int D) {
   return (size_t)p.B * p.Hkv * p.units_per_bh * p.nrep * (D + 4) * sizeof(float);
 }
@@ -1329,6 +1353,7 @@ extern "C" int sc_decode_attn(const ScDecodeArgs* args, void* workspace, size_t 
     return sc_fail(SC_ERR_WORKSPACE, "decode workspace too small: %zu < %zu bytes", workspace_bytes_, need);
   if (p.units_per_bh == 0) return sc_fail(SC_ERR_INVALID, "empty cache: no blocks and no tail scanned");
   p.ws = (float*)workspace;
+  p.young_slot = cus_per_xcd();
   hipStream_t s = (hipStream_t)stream;
   const int kk = args->tier->kp_keys, kv = args->tier->kp_values;
   // The branch-free path keeps one logit per lane, which needs GQA groups
