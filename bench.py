@@ -465,6 +465,37 @@ def model_loop(torch, device, prompt, decode_steps, layers=32):
     }
 
 
+def bench_block_pack(torch, hip, cache, reps=20):
+    """sc_tier_pack of every cold block of every sequence (one launch per
+    sequence), then sc_tier_unpack of the records back into the same slots;
+    HBM bytes = each byte read once and written once."""
+    B, nb = cache._B, cache.num_cold_blocks
+    rb = cache.block_record_bytes()
+    stream = ctypes.c_void_p(torch.cuda.current_stream().cuda_stream)
+    recs = [cache.export_blocks(b) for b in range(B)]
+    torch.cuda.synchronize()
+    e0, e1 = hip.event(), hip.event()
+    hip.record(e0, stream)
+    for _ in range(reps):
+        for b in range(B):
+            cache.export_blocks(b)
+    hip.record(e1, stream)
+    pack_ms = hip.elapsed_ms(e0, e1) / reps
+    hip.record(e0, stream)
+    for _ in range(reps):
+        for b in range(B):
+            cache.import_blocks(recs[b], seq=b, first=0)
+    hip.record(e1, stream)
+    unpack_ms = hip.elapsed_ms(e0, e1) / reps
+    total = B * nb * rb
+    return {"records": B * nb, "record_bytes": rb, "pack_us": round(pack_ms * 1e3, 1),
+            "pack_gbs": round(2 * total / (pack_ms * 1e-3) / 1e9, 1),
+            "unpack_us_incl_status_read": round(unpack_ms * 1e3, 1),
+            "unpack_gbs_incl_status_read": round(2 * total / (unpack_ms * 1e-3) / 1e9, 1),
+            "note": "pack: one launch per sequence; unpack: header check + copy + a host read of the status "
+                    "word per sequence (a synchronisation), so it is a lower bound on the kernels' rate"}
+
+
 TRAFFIC_JSON = os.path.join(HERE, "profiles", "decode_c3_traffic.json")
 
 
@@ -616,6 +647,8 @@ def main():
                                                      / cpu_rsvd["recon_err"], 5)
     others = None
     if not args.only_headline:
+        log("block wire format: pack / unpack of the batch-8 tiers")
+        wire = bench_block_pack(torch, hip, cache0)
         del caches, cache0
         torch.cuda.empty_cache()
         log("decode batch 1 (4K) and batch 16 (33K, with compression stall)")
@@ -623,6 +656,7 @@ def main():
             "batch1_ctx4096": decode_config(torch, lib, hip, device, 1, 7, 16, 512, args.rotate, 1000, 200),
             "batch16_ctx33280": decode_config(torch, lib, hip, device, 16, 64, 32, 512, 2, 300, 100,
                                               on_device=True, stall=True),
+            "block_wire_format": wire,
         }
     res = {
         "metric": "decode attn µs/layer + HBM GB/s (% peak) at 16K ctx; rSVD blocks/sec",

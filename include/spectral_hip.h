@@ -31,7 +31,7 @@
 extern "C" {
 #endif
 
-#define SC_ABI_VERSION 2
+#define SC_ABI_VERSION 3
 
 #define SC_OK 0
 #define SC_ERR_INVALID (-1)      /* bad argument / shape */
@@ -255,6 +255,64 @@ int sc_tier_compress(const ScTierDesc* tier, int32_t max_new_blocks, int32_t n_i
  */
 int sc_tier_dequant(const ScTierDesc* tier, int32_t first, int32_t count, void* k_out,
                     void* v_out, void* stream);
+
+/*
+ * Wire format of one cold block of one sequence, for offload and
+ * checkpoints.  The reference has no serialised form: its SpectralBlock
+ * (spectral_cache.py:20-46) lives only as torch tensors, and
+ * get_memory_stats (spectral_cache.py:614-655) only counts their bytes.
+ * A record is this 64-byte header followed by eight sections, each at a
+ * 16-byte aligned offset from the record start (offsets[] below):
+ *   0 codes_k   int8 [kv_heads][block_size][kp_keys]
+ *   1 codes_v   int8 [kv_heads][kp_values][block_size]
+ *   2 scales_k  fp32 [kv_heads][block_size] (PER_ROW) or [kv_heads]
+ *   3 scales_v  fp32 likewise
+ *   4 basis_k   fp16 [kv_heads][head_dim][kp_keys]
+ *   5 basis_v   fp16 [kv_heads][head_dim][kp_values]
+ *   6 minmax    fp32 [2][kv_heads][2] (K, then V; reference [min, max])
+ *   7 vnorm     fp32 [kv_heads]
+ * All fields little-endian; record_bytes is a multiple of 16, so records
+ * follow each other without padding.
+ */
+#define SC_BLOCK_MAGIC 0x31424353u /* "SCB1" */
+#define SC_BLOCK_VERSION 1
+#define SC_BLOCK_SECTIONS 8
+typedef struct ScBlockHeader {
+  uint32_t magic;
+  uint16_t version, header_bytes;
+  uint32_t record_bytes;
+  uint16_t kv_heads, head_dim, block_size;
+  uint16_t k_keys, k_values, kp_keys, kp_values;
+  uint8_t granularity, reserved;
+  int32_t start_position;
+  uint32_t offsets[SC_BLOCK_SECTIONS];
+} ScBlockHeader;
+
+/* Bytes of one block record for this tier geometry (host only, no GPU). */
+size_t sc_block_record_bytes(const ScTierDesc* tier);
+
+/*
+ * Pack cold blocks [first_block, first_block + n_blocks) of sequence `seq`
+ * into n_blocks consecutive records at dst (device memory, 16-byte
+ * aligned, >= n_blocks * sc_block_record_bytes bytes), headers included.
+ * The blocks must be in use (checked against nothing on the device: the
+ * caller knows its counters).
+ */
+int sc_tier_pack(const ScTierDesc* tier, int32_t seq, int32_t first_block, int32_t n_blocks, void* dst,
+                 size_t dst_bytes, void* stream);
+
+/*
+ * Unpack n_blocks records at src (device memory, 16-byte aligned) into cold
+ * slots [first_block, first_block + n_blocks) of sequence `seq`: codes,
+ * scales, bases, minmax, vnorm and block_start (the record's
+ * start_position); NCOLD becomes at least first_block + n_blocks.  Every
+ * header is checked on the device against the tier geometry first; if any
+ * does not match, nothing is written and *status (device int32, cleared by
+ * this call) receives SC_ERR_INVALID.  *status is 0 when the records were
+ * taken.
+ */
+int sc_tier_unpack(const ScTierDesc* tier, int32_t seq, int32_t first_block, int32_t n_blocks,
+                   const void* src, size_t src_bytes, int32_t* status, void* stream);
 
 const char* sc_last_error(void);
 int sc_abi_version(void);

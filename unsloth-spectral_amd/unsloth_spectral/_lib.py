@@ -12,7 +12,7 @@ import torch
 _HERE = os.path.dirname(os.path.abspath(__file__))
 LIB_PATH = os.path.join(_HERE, "libspectral_hip.so")
 
-ABI_VERSION = 2  # SC_ABI_VERSION of include/spectral_hip.h
+ABI_VERSION = 3  # SC_ABI_VERSION of include/spectral_hip.h
 SC_OK = 0
 SC_ROPE_ABSOLUTE, SC_ROPE_DISTANCE, SC_ROPE_NONE = 0, 1, 2
 SC_QUANT_PER_HEAD, SC_QUANT_PER_ROW, SC_QUANT_PER_TENSOR = 0, 1, 2
@@ -79,6 +79,10 @@ PROTOTYPES = {
     "sc_tier_append": (c_i32, [ctypes.POINTER(ScTierDesc), c_vp, c_vp, c_i64, c_i64, c_i64, c_vp, c_i32, c_vp]),
     "sc_tier_compress": (c_i32, [ctypes.POINTER(ScTierDesc), c_i32, c_i32, c_i32, c_u64, c_vp]),
     "sc_tier_dequant": (c_i32, [ctypes.POINTER(ScTierDesc), c_i32, c_i32, c_vp, c_vp, c_vp]),
+    "sc_block_record_bytes": (ctypes.c_size_t, [ctypes.POINTER(ScTierDesc)]),
+    "sc_tier_pack": (c_i32, [ctypes.POINTER(ScTierDesc), c_i32, c_i32, c_i32, c_vp, ctypes.c_size_t, c_vp]),
+    "sc_tier_unpack": (c_i32, [ctypes.POINTER(ScTierDesc), c_i32, c_i32, c_i32, c_vp, ctypes.c_size_t, c_vp,
+                               c_vp]),
     "sc_last_error": (ctypes.c_char_p, []),
     "sc_abi_version": (c_i32, []),
 }

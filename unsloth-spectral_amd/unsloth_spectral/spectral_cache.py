@@ -413,6 +413,116 @@ class SpectralCache:
         return (f"SpectralCache(tokens={self.total_tokens}, blocks={s['num_blocks']}, "
                 f"compression={s['compression_ratio']:.2f}x)")
 
+    # ------------------------------------------------------------ wire format
+    # No counterpart in the reference (its blocks are Python objects,
+    # spectral_cache.py:20-46); records: unsloth_spectral.wire.
+    def block_record_bytes(self) -> int:
+        """Bytes of one cold-block record of this cache's geometry."""
+        d = _lib.ScTierDesc()
+        d.batch, d.kv_heads, d.head_dim, d.block_size = 1, self.num_heads, self.head_dim, self.block_size
+        d.k_keys, d.k_values, d.kp_keys, d.kp_values = self.k_rank_keys, self.k_rank_values, self.kp_keys, \
+            self.kp_values
+        d.granularity = _lib.GRANULARITY[self.quant_granularity]
+        return int(_lib.load().sc_block_record_bytes(ctypes.byref(d)))
+
+    def export_blocks(self, seq: int = 0, first: int = 0, count: Optional[int] = None) -> torch.Tensor:
+        """Cold blocks [first, first + count) of sequence ``seq`` packed into
+        consecutive records (uint8 device tensor) by sc_tier_pack; count
+        defaults to every block from ``first`` on."""
+        rb = self.block_record_bytes()
+        n = (self._n_cold - first) if count is None else count
+        if self._B is None or n <= 0:
+            return torch.empty(0, dtype=torch.uint8, device=self.device)
+        if not 0 <= seq < self._B or first < 0 or first + n > self._n_cold:
+            raise ValueError(f"blocks [{first}, {first + n}) of sequence {seq} are not all in use "
+                             f"({self._n_cold} cold blocks, {self._B} sequences)")
+        out = torch.empty(n * rb, dtype=torch.uint8, device=self.device)
+        st = ctypes.c_void_p(torch.cuda.current_stream(self.device).cuda_stream)
+        check(_lib.load().sc_tier_pack(ctypes.byref(self._tier()), seq, first, n, ptr(out), out.numel(), st))
+        return out
+
+    def import_blocks(self, records: torch.Tensor, seq: int = 0, first: Optional[int] = None) -> int:
+        """Unpacks block records (uint8 tensor, host or device) into cold
+        slots first, first + 1, ... of sequence ``seq`` (default: after the
+        blocks in use) by sc_tier_unpack; returns the number of blocks.
+        If any record's header does not match this cache's geometry
+        (checked on the device) nothing is written and SpectralHIPError is
+        raised."""
+        if self._B is None:
+            raise ValueError("the cache holds no sequences yet (append or construct with batch_size)")
+        rb = self.block_record_bytes()
+        if records.dtype != torch.uint8 or records.dim() != 1 or records.numel() % rb:
+            raise ValueError(f"records must be a flat uint8 tensor of whole {rb}-byte records")
+        n = records.numel() // rb
+        if not 0 <= seq < self._B:
+            raise ValueError(f"sequence {seq} outside [0, {self._B})")
+        first = self._n_cold if first is None else first
+        if n == 0:
+            return 0
+        self._grow_cold(first + n)
+        buf = records.to(self.device)
+        if buf.data_ptr() % 16:
+            buf = buf.clone()
+        status = torch.zeros(1, dtype=torch.int32, device=self.device)
+        st = ctypes.c_void_p(torch.cuda.current_stream(self.device).cuda_stream)
+        check(_lib.load().sc_tier_unpack(ctypes.byref(self._tier()), seq, first, n, ptr(buf), buf.numel(),
+                                         ptr(status), st))
+        code = int(status.item())
+        if code:
+            raise _lib.SpectralHIPError(f"block records do not match this cache's geometry (code {code}); "
+                                        "none were taken")
+        self._n_cold = max(self._n_cold, first + n)
+        return n
+
+    def save(self, path: str):
+        """Writes the cache (every sequence's cold blocks as records, the FP16
+        tails and the counters) to a safetensors file."""
+        import json
+        from safetensors.torch import save_file
+        if self._B is None:
+            raise ValueError("nothing to save: the cache holds no sequences")
+        ncold = self.counters[:, _lib.SC_CNT_NCOLD].tolist()
+        tensors = {"counters": self.counters.cpu(), "tail_k": self.tail_k.cpu(), "tail_v": self.tail_v.cpu(),
+                   "tail_pos": self.tail_pos.cpu()}
+        for b in range(self._B):
+            tensors[f"blocks.{b}"] = self.export_blocks(b, 0, ncold[b]).cpu()
+        meta = {"num_heads": self.num_heads, "head_dim": self.head_dim, "block_size": self.block_size,
+                "k_rank_keys": self.k_rank_keys, "k_rank_values": self.k_rank_values,
+                "hot_buffer_size": self.hot_buffer_size, "quant_granularity": self.quant_granularity,
+                "oversampling": self.oversampling, "n_iter": self.n_iter, "seed": self.seed,
+                "batch": self._B, "tail_capacity": self._tail_cap, "n_cold": self._n_cold,
+                "tail_len": self._tail_len, "tail_head": self._tail_head, "total_tokens": self.total_tokens,
+                "current_position": self.current_position, "compression_count": self.compression_count,
+                "compress_calls": self._compress_calls}
+        save_file(tensors, path, metadata={"format": "spectral-cache/1", "cache": json.dumps(meta)})
+
+    @classmethod
+    def load(cls, path: str, device="cuda") -> "SpectralCache":
+        """Reads a file written by save()."""
+        import json
+        from safetensors import safe_open
+        with safe_open(path, framework="pt") as f:
+            meta = f.metadata() or {}
+            if meta.get("format") != "spectral-cache/1":
+                raise ValueError(f"{path} is not a saved SpectralCache")
+            m = json.loads(meta["cache"])
+            tensors = {k: f.get_tensor(k) for k in f.keys()}
+        c = cls(m["num_heads"], m["head_dim"], block_size=m["block_size"], k_rank_keys=m["k_rank_keys"],
+                k_rank_values=m["k_rank_values"], hot_buffer_size=m["hot_buffer_size"], device=device,
+                batch_size=m["batch"], max_blocks=max(1, m["n_cold"]), tail_capacity=m["tail_capacity"],
+                quant_granularity=m["quant_granularity"], oversampling=m["oversampling"], n_iter=m["n_iter"],
+                seed=m["seed"])
+        for b in range(m["batch"]):
+            c.import_blocks(tensors[f"blocks.{b}"], seq=b, first=0)
+        c.tail_k.copy_(tensors["tail_k"])
+        c.tail_v.copy_(tensors["tail_v"])
+        c.tail_pos.copy_(tensors["tail_pos"])
+        c.counters.copy_(tensors["counters"])
+        c._n_cold, c._tail_len, c._tail_head = m["n_cold"], m["tail_len"], m["tail_head"]
+        c.total_tokens, c.current_position = m["total_tokens"], m["current_position"]
+        c.compression_count, c._compress_calls = m["compression_count"], m["compress_calls"]
+        return c
+
     # ------------------------------------------------------------ construction from explicit tiers
     @classmethod
     def from_tiers(cls, codes_k, scales_k, basis_k, codes_v, scales_v, basis_v, block_start,
