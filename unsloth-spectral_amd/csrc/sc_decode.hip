@@ -1012,28 +1012,39 @@ __device__ void cold_unit(const DecodeParams& p, int b, int hq, int j, char* sme
   };
   using TT = std::integral_constant<bool, true>;
   using FF = std::integral_constant<bool, false>;
-  if (nR > 1) {
+  if (nR > 2) {
     step(TT(), FF(), 0);
-    for (int rr = 1; rr + 1 < nR; ++rr) step(TT(), TT(), rr);
+    for (int rr = 1; rr + 2 < nR; ++rr) step(TT(), TT(), rr);
   }
-  // the first FP16 tail tile of this workgroup is loaded during the last range
+  // the FP16 tail tile of this workgroup is loaded during the last two
+  // ranges and the V basis of the final projection during the last one (the
+  // basis too would spill registers in the second-to-last)
   TailFetch<D> tf;
   const int tl = p.counters[b * SC_NCOUNTERS + SC_CNT_TAIL_LEN];
   const bool has_tail = p.fold_tail && hvalid && j * kTile < tl;
   tail_fetch<D>(p, b, h, j * kTile, tl, p.counters[b * SC_NCOUNTERS + SC_CNT_TAIL_HEAD], has_tail, tf);
-  // the V basis of the final projection is loaded during the last range too
   half4_t bvf[G::MT][NT];
   const h16* bvb = p.basis_v + bhj * (long)D * KV;
+  auto load_bv = [&]() __attribute__((always_inline)) {
 #pragma unroll
-  for (int mt = 0; mt < G::MT; ++mt)
+    for (int mt = 0; mt < G::MT; ++mt)
 #pragma unroll
-    for (int nt = 0; nt < NT; ++nt)
-      bvf[mt][nt] = *reinterpret_cast<const half4_t*>(bvb + (long)(16 * mt + n) * KV + 16 * nt + 4 * g);
-  if (nR > 1)
+      for (int nt = 0; nt < NT; ++nt)
+        bvf[mt][nt] = *reinterpret_cast<const half4_t*>(bvb + (long)(16 * mt + n) * KV + 16 * nt + 4 * g);
+  };
+  if (nR > 2) {
+    step(TT(), TT(), nR - 2);
+    load_bv();
     step(FF(), TT(), nR - 1);
-  else
+  } else if (nR == 2) {
+    step(TT(), FF(), 0);
+    load_bv();
+    step(FF(), TT(), 1);
+  } else {
+    load_bv();
     step(FF(), FF(), 0);
-  tail_fetch_rope<D, HE>(p, rope, tf);  // positions arrived during the last range (unconditional: no branch)
+  }
+  tail_fetch_rope<D, HE>(p, rope, tf);  // positions arrived during the last ranges (unconditional: no branch)
   if (hvalid) range_values<KV, TPW, GEN, PRM, false>(p, cb0, CodeSrc{}, lgp, msp, alp, vn, st);
   if (!hvalid) return;
   // ---- FP16 tail tiles of this workgroup, merged into the running state
