@@ -20,6 +20,9 @@ absolute RoPE theta 1e6, one FP32 INT8 scale per row, 512-token blocks):
           append + compress + decode, minus a step that does not compress).
   rsvd    8 x 512 x 128 FP16 blocks of the same distribution, k=16, p=5, q=2,
           per-row INT8 quantisation; blocks/sec = matrices per second.
+  prefill  one layer of an 8192-token prompt (batch 1) attending causally over
+          its 16 cold blocks (k=16): the HIP prefill kernel against the dense
+          reference path (get_kv + fp16 attention).
   model loop (--model-loop, separate JSON line)  transformers
           MistralForCausalLM with Mistral-7B's shape (32 layers, hidden 4096,
           32/8 heads, FFN 14336, vocab 32768), random FP16 weights, patched
@@ -496,6 +499,44 @@ def bench_block_pack(torch, hip, cache, reps=20):
                     "word per sequence (a synchronisation), so it is a lower bound on the kernels' rate"}
 
 
+def bench_prefill(torch, hip, device, ctx=8192, k=16, reps=5):
+    """One layer's prefill attention of a ctx-token prompt (batch 1, 32/8
+    heads, causal) over its spectral tiers (ctx / 512 cold blocks of rank
+    k): the HIP prefill kernel against the dense reference path (get_kv,
+    apply_rope, fp16 attention in 1024-row slices)."""
+    from unsloth_spectral._prefill import run_prefill
+    from unsloth_spectral.integration import _dense_prefill
+    nblk = ctx // TB
+    cache, raw, _ = build_decode(torch, device, 1, nblk, k, 0, on_device=True)
+    del raw
+    cos, sin = rope_tables(torch, ctx + 64, device)
+    g = torch.Generator(device=device)
+    g.manual_seed(13)
+    Q = torch.randn(1, HQ, ctx, D, generator=g, device=device).half()
+    pos = torch.arange(ctx, device=device)[None]
+    stream = ctypes.c_void_p(torch.cuda.current_stream().cuda_stream)
+
+    def timed(fn):
+        fn()
+        torch.cuda.synchronize()
+        e0, e1 = hip.event(), hip.event()
+        hip.record(e0, stream)
+        for _ in range(reps):
+            out = fn()
+        hip.record(e1, stream)
+        return hip.elapsed_ms(e0, e1) / reps, out
+
+    ms_k, out_k = timed(lambda: run_prefill(Q, cache, cos, sin, pos))
+    ms_d, out_d = timed(lambda: _dense_prefill(Q, cache, cos, sin, HQ // HKV, None, 1.0 / math.sqrt(D), pos))
+    err = (out_k.float() - out_d.float()).abs().max().item()
+    flops = 2 * 2 * HQ * D * ctx * (ctx + 1) / 2  # causal QK^T and PV
+    return {"context": ctx, "cold_blocks": nblk, "rank": k, "batch": 1, "kernel_ms": round(ms_k, 3),
+            "dense_reference_path_ms": round(ms_d, 3), "speedup": round(ms_d / ms_k, 2),
+            "attention_tflops": round(flops / (ms_k * 1e-3) / 1e12, 1),
+            "mfma_fp16_frac": round(flops / (ms_k * 1e-3) / (MFMA_FP16_PEAK_TFLOPS * 1e12), 4),
+            "max_abs_diff_vs_dense": round(err, 5)}
+
+
 TRAFFIC_JSON = os.path.join(HERE, "profiles", "decode_c3_traffic.json")
 
 
@@ -658,6 +699,8 @@ def main():
                                               on_device=True, stall=True),
             "block_wire_format": wire,
         }
+        log("prefill attention, 8192-token prompt over 16 cold blocks")
+        others["prefill_ctx8192"] = bench_prefill(torch, hip, device)
     res = {
         "metric": "decode attn µs/layer + HBM GB/s (% peak) at 16K ctx; rSVD blocks/sec",
         "value": round(nb / (ms_per_step * 1e-3) / 1e9, 2),

@@ -31,7 +31,7 @@
 extern "C" {
 #endif
 
-#define SC_ABI_VERSION 3
+#define SC_ABI_VERSION 4
 
 #define SC_OK 0
 #define SC_ERR_INVALID (-1)      /* bad argument / shape */
@@ -255,6 +255,44 @@ int sc_tier_compress(const ScTierDesc* tier, int32_t max_new_blocks, int32_t n_i
  */
 int sc_tier_dequant(const ScTierDesc* tier, int32_t first, int32_t count, void* k_out,
                     void* v_out, void* stream);
+
+/*
+ * Prefill attention: t_q query tokens per sequence attend over every tier
+ * of the cache (cold blocks and FP16 tail) with a causal mask (a key is
+ * kept iff its position <= the query's position), without materialising
+ * keys or values.  Replaces the reference's prefill path
+ * (integration.py:292-346: get_kv, apply_rope at the keys' absolute
+ * positions with the first half of the cos/sin rows, dense fp16 attention,
+ * softmax in fp32).
+ *   q          fp16 [batch][q_heads][t_q][128] post-RoPE, element strides
+ *              (16-byte aligned rows)
+ *   query_pos  int32 [batch][t_q] absolute positions (row stride
+ *              query_pos_stride_b)
+ *   cos/sin    fp16 [rope_len][128] (row stride rope_stride; only the first
+ *              64 columns are read; positions >= rope_len read the last row,
+ *              so the tables must cover every cached position)
+ *   out        fp16 [batch][q_heads][t_q][128], element strides
+ * Supported: head_dim 128, 4 query heads per KV head, padded ranks 16/32/64,
+ * block_size a multiple of 16.
+ */
+typedef struct ScPrefillArgs {
+  const ScTierDesc* tier;
+  int32_t q_heads;
+  int32_t t_q;
+  float scale;
+  const void* q;
+  int64_t q_stride_b, q_stride_h, q_stride_t;
+  const int32_t* query_pos;
+  int64_t query_pos_stride_b;
+  const void* cos;
+  const void* sin;
+  int64_t rope_stride;
+  int32_t rope_len;
+  void* out;
+  int64_t out_stride_b, out_stride_h, out_stride_t;
+} ScPrefillArgs;
+
+int sc_prefill_attn(const ScPrefillArgs* args, void* stream);
 
 /*
  * Wire format of one cold block of one sequence, for offload and

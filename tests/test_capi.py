@@ -24,7 +24,7 @@ def test_header_declares_the_api():
     names = _declared_functions()
     for fn in ("sc_decode_attn", "sc_decode_workspace_size", "sc_rsvd_compress", "sc_quantize_int8",
                "sc_tier_append", "sc_tier_compress", "sc_tier_dequant", "sc_last_error", "sc_abi_version",
-                 "sc_block_record_bytes", "sc_tier_pack", "sc_tier_unpack"):
+                 "sc_block_record_bytes", "sc_tier_pack", "sc_tier_unpack", "sc_prefill_attn"):
         assert fn in names
 
 
@@ -36,7 +36,7 @@ def test_library_exports_every_declared_symbol():
     for fn in _declared_functions():
         assert hasattr(lib, fn), fn
     assert set(_lib.PROTOTYPES) == _declared_functions()
-    assert _lib.load().sc_abi_version() == _lib.ABI_VERSION == 3
+    assert _lib.load().sc_abi_version() == _lib.ABI_VERSION == 4
 
 
 def test_struct_layouts_match_header():

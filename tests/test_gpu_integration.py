@@ -12,9 +12,9 @@ the append) and then attends (integration.py:596-659).
     fp16 attention) must equal the unpatched fp32 model's (run on the CPU)
     within the noise of the fp16 attention.
   * Cold blocks, with a block boundary crossed during decode: the logits of
-    the HIP decode kernel must equal those of dense attention over the
-    cache's own reconstruction (use_spectral_attention=False, which is the
-    reference's dense fallback over get_kv, integration.py:353-402).
+    the HIP prefill and decode kernels must equal those of dense attention
+    over the cache's own reconstruction (use_spectral_attention=False, which
+    is the reference's dense path over get_kv, integration.py:292-402).
 """
 import pytest
 import torch
@@ -111,7 +111,9 @@ def test_cold_blocks_and_decode_compression_match_dense_over_tiers():
     reset_spectral_caches(model)
     patch_unsloth_attention(model, use_spectral_attention=False, verbose=False)
     dense = _run_patched(model, ids, n_prompt)
-    assert torch.equal(kernel[0], dense[0])       # same prefill path on both sides
+    err0 = _rel(kernel[:1], dense[:1])             # prefill: HIP prefill kernel vs dense over get_kv
+    print(f"prefill kernel vs dense over the reconstruction: {err0:.2e}")
+    assert err0 < 1e-2
     err = _rel(kernel, dense)
     print(f"decode kernel vs dense over the reconstruction: {err:.2e}")
     assert err < 1e-2

@@ -1,0 +1,384 @@
+// Spectral prefill attention (gfx950): a chunk of query tokens attends over
+// every tier of the cache -- cold blocks (INT8 codes + fp16 bases) and the
+// FP16 tail -- with a causal mask, without materialising the keys and
+// values (the reference's prefill path reconstructs them all with get_kv
+// and runs dense attention, integration.py:292-346; keys are rotated at
+// their absolute positions with apply_rope, spectral_attention.py:80-114,
+// which uses the first half of the cos/sin rows for both halves).
+//
+// Workgroup = (sequence b, KV head h, 16 query tokens); its four waves are
+// the four query heads of h (GQA group of 4).  Per 16-token key tile:
+//   * cold block: the waves reconstruct K^T = B_K . C^T on MFMA from the
+//     INT8 codes (coefficients fp16(code * scale), as the reference stores
+//     them), two 16-row d tiles each (d and d + 64, so every RoPE pair is
+//     in one wave), round to fp16, rotate, and write K[tok][d] to LDS;
+//     tail: the rows come from the FP16 ring and are rotated the same way;
+//   * each wave forms S^T = K . Q^T (16 keys x its 16 queries) on MFMA,
+//     rounds it like the reference (fp16 scores, then fp16 after the
+//     scaling), masks keys after the query's position, and folds the tile
+//     into an online softmax (fp32, base e);
+//   * values: cold blocks accumulate O_k^T += C_V^T . P^T in rank space and
+//     project O_d^T += B_V^T . O_k^T once per block (hi/lo fp16 split of
+//     O_k); tail tiles add V^T . P^T directly, V^T read from LDS with
+//     transposing reads.
+// MFMA 16x16 layouts: output lane (g, n) holds D[4g + j][n]; operand lane
+// (g, n) supplies row/column n and the K slots of group g.
+#include "sc_common.h"
+
+namespace {
+
+constexpr int kThreads = 256;
+constexpr int kQT = 16;            // query tokens per workgroup
+constexpr int kKT = 16;            // key tokens per tile
+constexpr int kPitch = 128 + 8;    // LDS row pitch (halves) of a K or V tile
+constexpr int kTile = kKT * kPitch;  // halves per LDS tile
+
+struct PrefillParams {
+  ScTierDesc t;
+  int Hq, Tq, nqt;
+  const h16* q;
+  long q_sb, q_sh, q_st;
+  const int32_t* qpos;  // [B][Tq]
+  long qpos_sb;
+  const h16* cos;
+  const h16* sin;
+  long rope_stride;
+  int rope_len;
+  float scale;
+  h16* out;
+  long o_sb, o_sh, o_st;
+};
+
+typedef short short4_t __attribute__((ext_vector_type(4)));
+typedef __attribute__((address_space(3))) short4_t lds_s4;
+
+// Rotate the (x1, x2) = (K[d], K[d + 64]) pairs of one lane (4 consecutive
+// d) at key position pos with apply_rope's formula in fp16 arithmetic
+// (each product and difference rounded, as torch does on fp16 tensors),
+// then store them as K[tok][d] into the LDS tile.
+__device__ __forceinline__ void rope_store(const PrefillParams& p, half4_t x1, half4_t x2, int pos, bool valid,
+                                           int d1, h16* krow) {
+  half4_t c = (half4_t)(h16)0, s = (half4_t)(h16)0;
+  if (valid) {
+    const long row = min(max(pos, 0), p.rope_len - 1);  // the host cannot see positions: never read past the table
+    c = *reinterpret_cast<const half4_t*>(p.cos + row * p.rope_stride + d1);
+    s = *reinterpret_cast<const half4_t*>(p.sin + row * p.rope_stride + d1);
+  }
+  half4_t o1, o2;
+#pragma unroll
+  for (int e = 0; e < 4; ++e) {
+    const h16 a = x1[e] * c[e], b = x2[e] * s[e];
+    const h16 a2 = x2[e] * c[e], b2 = x1[e] * s[e];
+    o1[e] = a - b;
+    o2[e] = a2 + b2;
+  }
+  *reinterpret_cast<half4_t*>(krow + d1) = o1;
+  *reinterpret_cast<half4_t*>(krow + d1 + 64) = o2;
+}
+
+template <int KK, int KV>
+__global__ __launch_bounds__(kThreads) void prefill_kernel(PrefillParams p) {
+  __shared__ __align__(16) h16 kbuf[2][kTile];
+  __shared__ __align__(16) h16 vbuf[2][kTile];
+  const ScTierDesc& t = p.t;
+  const int lane = threadIdx.x & 63, g = lane >> 4, n = lane & 15;
+  const int w = threadIdx.x >> 6;
+  const int qt = blockIdx.x % p.nqt;
+  const int bh = blockIdx.x / p.nqt;
+  const int b = bh / t.kv_heads, h = bh % t.kv_heads;
+  const int qh = h * 4 + w;
+  const int q0 = qt * kQT;
+  const int qi = q0 + n;  // this lane's query column
+  const bool qvalid = qi < p.Tq;
+  const int qpos = qvalid ? p.qpos[b * p.qpos_sb + qi] : -1;
+  // largest query position of the workgroup (keys beyond it are skipped)
+  int qmax = qpos;
+#pragma unroll
+  for (int o = 1; o < 16; o <<= 1) qmax = max(qmax, __shfl_xor(qmax, o));
+  // Q^T operand: lane (g, n) supplies Q[q n][32 s + 8 g .. +7]
+  half8_t qb[4];
+  {
+    const h16* qr = p.q + b * p.q_sb + (long)qh * p.q_sh + (long)(qvalid ? qi : 0) * p.q_st;
+#pragma unroll
+    for (int s = 0; s < 4; ++s)
+      qb[s] = qvalid ? *reinterpret_cast<const half8_t*>(qr + 32 * s + 8 * g) : (half8_t)(h16)0;
+  }
+  constexpr int NTV = KV / 16;
+  float m = -INFINITY, l = 0.f;
+  float4_t od[8], ok[NTV];
+#pragma unroll
+  for (int i = 0; i < 8; ++i) od[i] = (float4_t)0.f;
+#pragma unroll
+  for (int i = 0; i < NTV; ++i) ok[i] = (float4_t)0.f;
+  const int32_t* cnt = t.counters + b * SC_NCOUNTERS;
+  const int ncold = cnt[SC_CNT_NCOLD];
+  const bool per_row = t.granularity == SC_QUANT_PER_ROW;
+  int buf = 0;
+
+  // Scores of the tile in kbuf[buf], masked, folded into the softmax state;
+  // returns P^T (lane (g, n): P[tok 4g + j][q n]) as fp16.
+  auto scores = [&](const int (&kpos)[4]) __attribute__((always_inline)) -> half4_t {
+    float4_t sacc = (float4_t)0.f;
+    const h16* kr = kbuf[buf] + n * kPitch;
+#pragma unroll
+    for (int s = 0; s < 4; ++s)
+      sacc = mfma_16x16x32(*reinterpret_cast<const half8_t*>(kr + 32 * s + 8 * g), qb[s], sacc);
+    float sv[4];
+    float tmax = -INFINITY;
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      // reference rounding: fp16 matmul output, then fp16 after the scaling
+      const float s16 = (float)(h16)sacc[j];
+      float v = (float)(h16)(s16 * p.scale);
+      if (!qvalid || kpos[j] < 0 || kpos[j] > qpos) v = -INFINITY;
+      sv[j] = v;
+      tmax = fmaxf(tmax, v);
+    }
+    tmax = max_over_rows(tmax);
+    const float mn = fmaxf(m, tmax);
+    half4_t pp = (half4_t)(h16)0;
+    if (mn != -INFINITY) {
+      const float alpha = __expf(m - mn);  // m = -inf: 0
+      float ls = 0.f;
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        const float e = sv[j] == -INFINITY ? 0.f : __expf(sv[j] - mn);
+        pp[j] = (h16)e;
+        ls += e;
+      }
+      l = l * alpha + sum_over_rows(ls);
+#pragma unroll
+      for (int i = 0; i < 8; ++i) od[i] *= alpha;
+#pragma unroll
+      for (int i = 0; i < NTV; ++i) ok[i] *= alpha;
+      m = mn;
+    }
+    return pp;
+  };
+
+  // ---------------------------------------------------------------- cold blocks
+  for (int j = 0; j < ncold; ++j) {
+    const int start = t.block_start[(long)b * t.max_blocks + j];
+    if (start > qmax) continue;  // the whole block is after every query
+    const long bhj = ((long)b * t.kv_heads + h) * t.max_blocks + j;
+    const int8_t* ck = t.codes_k + bhj * t.block_size * KK;
+    const int8_t* cv = t.codes_v + bhj * KV * t.block_size;
+    const float* sk = t.scales_k + (per_row ? bhj * t.block_size : bhj);
+    const float* svp = t.scales_v + (per_row ? bhj * t.block_size : bhj);
+    const h16* bk = (const h16*)t.basis_k + bhj * 128 * KK;
+    const h16* bv = (const h16*)t.basis_v + bhj * 128 * KV;
+    // A operands of this wave's two d tiles: basis rows d = 16 mt + n, mt in {w, w + 4}
+    constexpr int KC = KK >= 32 ? KK / 32 : 1;
+    half8_t ak[2][KC];
+    half4_t ak4[2];
+#pragma unroll
+    for (int u = 0; u < 2; ++u) {
+      const h16* row = bk + (long)(16 * (w + 4 * u) + n) * KK;
+      if constexpr (KK == 16) {
+        ak4[u] = *reinterpret_cast<const half4_t*>(row + 4 * g);
+      } else {
+#pragma unroll
+        for (int c = 0; c < KC; ++c) ak[u][c] = *reinterpret_cast<const half8_t*>(row + 32 * c + 8 * g);
+      }
+    }
+    const int ntiles = t.block_size / kKT;
+    for (int tt = 0; tt < ntiles; ++tt) {
+      const int tok0 = tt * kKT;
+      if (start + tok0 > qmax) break;  // later tiles of this block are after every query
+      // ---- reconstruct this wave's d tiles of K^T for tokens tok0 .. tok0 + 15
+      const int tok = tok0 + n;
+      const float scl = per_row ? sk[tok] : sk[0];
+      float4_t x[2];
+#pragma unroll
+      for (int u = 0; u < 2; ++u) x[u] = (float4_t)0.f;
+      if constexpr (KK == 16) {
+        const uint32_t cw = *reinterpret_cast<const uint32_t*>(ck + (long)tok * KK + 4 * g);
+        half4_t cf;
+#pragma unroll
+        for (int e = 0; e < 4; ++e) cf[e] = (h16)((float)(int8_t)(cw >> (8 * e)) * scl);
+#pragma unroll
+        for (int u = 0; u < 2; ++u) x[u] = mfma_16x16x16(ak4[u], cf, x[u]);
+      } else {
+#pragma unroll
+        for (int c = 0; c < KC; ++c) {
+          const uint2 cw = *reinterpret_cast<const uint2*>(ck + (long)tok * KK + 32 * c + 8 * g);
+          half8_t cf;
+#pragma unroll
+          for (int e = 0; e < 4; ++e) {
+            cf[e] = (h16)((float)(int8_t)(cw.x >> (8 * e)) * scl);
+            cf[4 + e] = (h16)((float)(int8_t)(cw.y >> (8 * e)) * scl);
+          }
+#pragma unroll
+          for (int u = 0; u < 2; ++u) x[u] = mfma_16x16x32(ak[u][c], cf, x[u]);
+        }
+      }
+      // lane (g, n) holds K[tok n][16 mt + 4 g + j]: x[0] is d1 = 16 w + 4 g, x[1] is d1 + 64
+      half4_t x1, x2;
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        x1[e] = (h16)x[0][e];
+        x2[e] = (h16)x[1][e];
+      }
+      rope_store(p, x1, x2, start + tok, true, 16 * w + 4 * g, kbuf[buf] + n * kPitch);
+      __syncthreads();
+      int kpos[4];
+#pragma unroll
+      for (int e = 0; e < 4; ++e) kpos[e] = start + tok0 + 4 * g + e;
+      const half4_t pp = scores(kpos);
+      // ---- values in rank space: O_k^T[16 nt + n][q] += C_V[tok 4g + e][16 nt + n] * P[tok][q]
+      float4_t sv4;
+      if (per_row) {
+        sv4 = *reinterpret_cast<const float4_t*>(svp + tok0 + 4 * g);
+      } else {
+        sv4 = (float4_t)svp[0];
+      }
+#pragma unroll
+      for (int nt = 0; nt < NTV; ++nt) {
+        const uint32_t cw = *reinterpret_cast<const uint32_t*>(cv + (long)(16 * nt + n) * t.block_size + tok0 + 4 * g);
+        half4_t a;
+#pragma unroll
+        for (int e = 0; e < 4; ++e) a[e] = (h16)((float)(int8_t)(cw >> (8 * e)) * sv4[e]);
+        ok[nt] = mfma_16x16x16(a, pp, ok[nt]);
+      }
+      buf ^= 1;
+    }
+    // ---- projection of the block: O_d^T[d][q] += B_V[d][k] O_k^T[k][q] (hi + lo fp16 parts)
+    half4_t ph[NTV], pl[NTV];
+#pragma unroll
+    for (int nt = 0; nt < NTV; ++nt)
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        const h16 hi = (h16)ok[nt][e];
+        ph[nt][e] = hi;
+        pl[nt][e] = (h16)(ok[nt][e] - (float)hi);
+      }
+#pragma unroll
+    for (int mt = 0; mt < 8; ++mt)
+#pragma unroll
+      for (int nt = 0; nt < NTV; ++nt) {
+        const half4_t a = *reinterpret_cast<const half4_t*>(bv + (long)(16 * mt + n) * KV + 16 * nt + 4 * g);
+        od[mt] = mfma_16x16x16(a, ph[nt], od[mt]);
+        od[mt] = mfma_16x16x16(a, pl[nt], od[mt]);
+      }
+#pragma unroll
+    for (int i = 0; i < NTV; ++i) ok[i] = (float4_t)0.f;
+  }
+
+  // ---------------------------------------------------------------- FP16 tail
+  const int tl = cnt[SC_CNT_TAIL_LEN], thead = cnt[SC_CNT_TAIL_HEAD];
+  const h16* tk = (const h16*)t.tail_k + ((long)b * t.kv_heads + h) * t.tail_capacity * 128;
+  const h16* tv = (const h16*)t.tail_v + ((long)b * t.kv_heads + h) * t.tail_capacity * 128;
+  const int32_t* tp = t.tail_pos + (long)b * t.tail_capacity;
+  for (int tok0 = 0; tok0 < tl; tok0 += kKT) {
+    // lane (g, n): token tok0 + n, d chunk d1 = 16 w + 4 g (and d1 + 64) of K and V
+    const int i = tok0 + n;
+    const bool valid = i < tl;
+    const int slot = valid ? (thead + i) % t.tail_capacity : 0;
+    const int pos = valid ? tp[slot] : -1;
+    const int d1 = 16 * w + 4 * g;
+    half4_t x1 = (half4_t)(h16)0, x2 = x1, v1 = x1, v2 = x1;
+    if (valid) {
+      x1 = *reinterpret_cast<const half4_t*>(tk + (long)slot * 128 + d1);
+      x2 = *reinterpret_cast<const half4_t*>(tk + (long)slot * 128 + d1 + 64);
+      v1 = *reinterpret_cast<const half4_t*>(tv + (long)slot * 128 + d1);
+      v2 = *reinterpret_cast<const half4_t*>(tv + (long)slot * 128 + d1 + 64);
+    }
+    rope_store(p, x1, x2, pos, valid, d1, kbuf[buf] + n * kPitch);
+    *reinterpret_cast<half4_t*>(vbuf[buf] + n * kPitch + d1) = v1;
+    *reinterpret_cast<half4_t*>(vbuf[buf] + n * kPitch + d1 + 64) = v2;
+    __syncthreads();
+    int kpos[4];
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+      const int ii = tok0 + 4 * g + e;
+      kpos[e] = ii < tl ? tp[(thead + ii) % t.tail_capacity] : -1;
+    }
+    const half4_t pp = scores(kpos);
+    // O_d^T[16 mt + n][q] += V[tok 4g + e][16 mt + n] P[tok][q]; V^T by transposing reads:
+    // lane L of group g addresses row 4g + (L >> 2), columns 16 mt + 4 (L & 3)
+#pragma unroll
+    for (int mt = 0; mt < 8; ++mt) {
+      const h16* src = vbuf[buf] + (4 * g + (n >> 2)) * kPitch + 16 * mt + 4 * (n & 3);
+      const short4_t r = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_s4*)src);
+      od[mt] = mfma_16x16x16(__builtin_bit_cast(half4_t, r), pp, od[mt]);
+    }
+    buf ^= 1;
+  }
+
+  // ---------------------------------------------------------------- output
+  if (qvalid) {
+    const float il = l > 0.f ? 1.f / l : 0.f;
+    h16* o = p.out + b * p.o_sb + (long)qh * p.o_sh + (long)qi * p.o_st;
+#pragma unroll
+    for (int mt = 0; mt < 8; ++mt) {
+      half4_t v;
+#pragma unroll
+      for (int e = 0; e < 4; ++e) v[e] = (h16)(od[mt][e] * il);
+      *reinterpret_cast<half4_t*>(o + 16 * mt + 4 * g) = v;
+    }
+  }
+}
+
+template <int KK>
+int launch_kv(const PrefillParams& p, int kv, dim3 grid, hipStream_t s) {
+  switch (kv) {
+    case 16: hipLaunchKernelGGL((prefill_kernel<KK, 16>), grid, dim3(kThreads), 0, s, p); break;
+    case 32: hipLaunchKernelGGL((prefill_kernel<KK, 32>), grid, dim3(kThreads), 0, s, p); break;
+    default: hipLaunchKernelGGL((prefill_kernel<KK, 64>), grid, dim3(kThreads), 0, s, p); break;
+  }
+  return sc_launch_status("prefill_kernel");
+}
+
+}  // namespace
+
+extern "C" int sc_prefill_attn(const ScPrefillArgs* a, void* stream) {
+  if (!a || !a->tier) return sc_fail(SC_ERR_INVALID, "sc_prefill_attn: null arguments");
+  const ScTierDesc* t = a->tier;
+  if (t->head_dim != 128) return sc_fail(SC_ERR_UNSUPPORTED, "prefill: head_dim %d unsupported (128)", t->head_dim);
+  if (a->q_heads != 4 * t->kv_heads)
+    return sc_fail(SC_ERR_UNSUPPORTED, "prefill: GQA group %d unsupported (4 query heads per KV head)",
+                   t->kv_heads ? a->q_heads / t->kv_heads : 0);
+  const int kk = t->kp_keys, kv = t->kp_values;
+  if ((kk != 16 && kk != 32 && kk != 64) || (kv != 16 && kv != 32 && kv != 64))
+    return sc_fail(SC_ERR_UNSUPPORTED, "prefill: padded ranks must be 16, 32 or 64 (got %d, %d)", kk, kv);
+  if (t->block_size < kKT || t->block_size % kKT)
+    return sc_fail(SC_ERR_UNSUPPORTED, "prefill: block_size %d must be a multiple of %d", t->block_size, kKT);
+  if (a->t_q < 0) return sc_fail(SC_ERR_INVALID, "prefill: t_q %d < 0", a->t_q);
+  if (a->rope_len < 1) return sc_fail(SC_ERR_INVALID, "prefill: empty RoPE tables");
+  if (!a->q || !a->out || !a->query_pos || !a->cos || !a->sin)
+    return sc_fail(SC_ERR_INVALID, "prefill: null q / out / query_pos / cos / sin");
+  if (((uintptr_t)a->q & 15) || (a->q_stride_t % 8) || (a->q_stride_h % 8) || (a->q_stride_b % 8) ||
+      ((uintptr_t)a->out & 7) || (a->out_stride_t % 4) || ((uintptr_t)a->cos & 7) || ((uintptr_t)a->sin & 7) ||
+      (a->rope_stride % 4))
+    return sc_fail(SC_ERR_INVALID, "prefill: misaligned q / out / RoPE tables");
+  if (a->t_q == 0) return SC_OK;
+  PrefillParams p;
+  p.t = *t;
+  p.Hq = a->q_heads;
+  p.Tq = a->t_q;
+  p.nqt = (a->t_q + kQT - 1) / kQT;
+  p.q = (const h16*)a->q;
+  p.q_sb = a->q_stride_b;
+  p.q_sh = a->q_stride_h;
+  p.q_st = a->q_stride_t;
+  p.qpos = a->query_pos;
+  p.qpos_sb = a->query_pos_stride_b;
+  p.cos = (const h16*)a->cos;
+  p.sin = (const h16*)a->sin;
+  p.rope_stride = a->rope_stride;
+  p.rope_len = a->rope_len;
+  p.scale = a->scale;
+  p.out = (h16*)a->out;
+  p.o_sb = a->out_stride_b;
+  p.o_sh = a->out_stride_h;
+  p.o_st = a->out_stride_t;
+  const long nwg = (long)t->batch * t->kv_heads * p.nqt;
+  if (nwg > 0x7fffffffL) return sc_fail(SC_ERR_UNSUPPORTED, "prefill: grid too large");
+  const dim3 grid((unsigned)nwg);
+  hipStream_t s = (hipStream_t)stream;
+  switch (kk) {
+    case 16: return launch_kv<16>(p, kv, grid, s);
+    case 32: return launch_kv<32>(p, kv, grid, s);
+    default: return launch_kv<64>(p, kv, grid, s);
+  }
+}

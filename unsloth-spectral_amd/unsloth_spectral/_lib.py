@@ -12,7 +12,7 @@ import torch
 _HERE = os.path.dirname(os.path.abspath(__file__))
 LIB_PATH = os.path.join(_HERE, "libspectral_hip.so")
 
-ABI_VERSION = 3  # SC_ABI_VERSION of include/spectral_hip.h
+ABI_VERSION = 4  # SC_ABI_VERSION of include/spectral_hip.h
 SC_OK = 0
 SC_ROPE_ABSOLUTE, SC_ROPE_DISTANCE, SC_ROPE_NONE = 0, 1, 2
 SC_QUANT_PER_HEAD, SC_QUANT_PER_ROW, SC_QUANT_PER_TENSOR = 0, 1, 2
@@ -54,6 +54,16 @@ class ScDecodeArgs(ctypes.Structure):
     ]
 
 
+class ScPrefillArgs(ctypes.Structure):
+    _fields_ = [
+        ("tier", ctypes.POINTER(ScTierDesc)), ("q_heads", c_i32), ("t_q", c_i32), ("scale", c_f32),
+        ("q", c_vp), ("q_stride_b", c_i64), ("q_stride_h", c_i64), ("q_stride_t", c_i64),
+        ("query_pos", c_vp), ("query_pos_stride_b", c_i64),
+        ("cos", c_vp), ("sin", c_vp), ("rope_stride", c_i64), ("rope_len", c_i32),
+        ("out", c_vp), ("out_stride_b", c_i64), ("out_stride_h", c_i64), ("out_stride_t", c_i64),
+    ]
+
+
 class ScCompressArgs(ctypes.Structure):
     _fields_ = [
         ("count", c_i32), ("inner", c_i32), ("rows", c_i32), ("cols", c_i32), ("rank", c_i32),
@@ -79,6 +89,7 @@ PROTOTYPES = {
     "sc_tier_append": (c_i32, [ctypes.POINTER(ScTierDesc), c_vp, c_vp, c_i64, c_i64, c_i64, c_vp, c_i32, c_vp]),
     "sc_tier_compress": (c_i32, [ctypes.POINTER(ScTierDesc), c_i32, c_i32, c_i32, c_u64, c_vp]),
     "sc_tier_dequant": (c_i32, [ctypes.POINTER(ScTierDesc), c_i32, c_i32, c_vp, c_vp, c_vp]),
+    "sc_prefill_attn": (c_i32, [ctypes.POINTER(ScPrefillArgs), c_vp]),
     "sc_block_record_bytes": (ctypes.c_size_t, [ctypes.POINTER(ScTierDesc)]),
     "sc_tier_pack": (c_i32, [ctypes.POINTER(ScTierDesc), c_i32, c_i32, c_i32, c_vp, ctypes.c_size_t, c_vp]),
     "sc_tier_unpack": (c_i32, [ctypes.POINTER(ScTierDesc), c_i32, c_i32, c_i32, c_vp, ctypes.c_size_t, c_vp,

@@ -11,8 +11,10 @@ to the layer's SpectralCache (compression fires inside append), then attend.
 One-token decode steps run the fused HIP kernel over all tiers (cold blocks
 and FP16 tail, so the reference's ``total_tokens > block_size`` branch and
 its dense fallback are the same kernel with zero or more cold blocks).
-Multi-token (prefill) steps run dense causal attention over the cache's
-reconstruction (``get_kv``), as the reference does (:292-346).
+Multi-token (prefill) steps attend causally over every tier with the HIP
+prefill kernel (tiles reconstructed on the fly); the reference's dense
+attention over ``get_kv`` (:292-346) remains for geometries the kernel does
+not take and for ``use_spectral_attention=False``.
 
 The patched forward accepts the attention signature of transformers 5.x
 (``position_embeddings=(cos, sin)`` for the current tokens, cache in the
@@ -28,6 +30,7 @@ import torch.nn.functional as F
 
 from . import _lib
 from ._decode import run_decode
+from ._prefill import prefill_supported, run_prefill
 from .spectral_attention import apply_rope, repeat_kv as _repeat_kv
 from .spectral_cache import SpectralCache
 
@@ -160,6 +163,9 @@ def _attend(self, hidden_states, cos_cur, sin_cur, position_ids, attention_mask,
     if T == 1 and opts["use_spectral_attention"]:
         qpos = position_ids[:, -1]
         out = run_decode(q_rot, cache, cos_tab, sin_tab, qpos, None, scale, rope_mode, halves_equal=True)
+    elif opts["use_spectral_attention"] and prefill_supported(cache, Hq) and (B == 1 or attention_mask is None):
+        # causal by positions; a padding mask (batch > 1 with a mask) takes the dense path
+        out = run_prefill(q_rot, cache, cos_tab, sin_tab, position_ids, scale)
     else:
         out = _dense_prefill(q_rot, cache, cos_tab, sin_tab, Hq // Hkv, attention_mask, scale, position_ids)
     out = out.to(hidden_states.dtype).transpose(1, 2).reshape(B, T, Hq * D)
