@@ -53,17 +53,11 @@ typedef short short4_t __attribute__((ext_vector_type(4)));
 typedef __attribute__((address_space(3))) short4_t lds_s4;
 
 // Rotate the (x1, x2) = (K[d], K[d + 64]) pairs of one lane (4 consecutive
-// d) at key position pos with apply_rope's formula in fp16 arithmetic
-// (each product and difference rounded, as torch does on fp16 tensors),
-// then store them as K[tok][d] into the LDS tile.
-__device__ __forceinline__ void rope_store(const PrefillParams& p, half4_t x1, half4_t x2, int pos, bool valid,
-                                           int d1, h16* krow) {
-  half4_t c = (half4_t)(h16)0, s = (half4_t)(h16)0;
-  if (valid) {
-    const long row = min(max(pos, 0), p.rope_len - 1);  // the host cannot see positions: never read past the table
-    c = *reinterpret_cast<const half4_t*>(p.cos + row * p.rope_stride + d1);
-    s = *reinterpret_cast<const half4_t*>(p.sin + row * p.rope_stride + d1);
-  }
+// d) with apply_rope's formula in fp16 arithmetic (each product and
+// difference rounded, as torch does on fp16 tensors; c, s = the first-half
+// cos / sin at the key's position), then store them as K[tok][d] into the
+// LDS tile row.
+__device__ __forceinline__ void rope_rotate_store(half4_t x1, half4_t x2, half4_t c, half4_t s, int d1, h16* krow) {
   half4_t o1, o2;
 #pragma unroll
   for (int e = 0; e < 4; ++e) {
@@ -74,6 +68,14 @@ __device__ __forceinline__ void rope_store(const PrefillParams& p, half4_t x1, h
   }
   *reinterpret_cast<half4_t*>(krow + d1) = o1;
   *reinterpret_cast<half4_t*>(krow + d1 + 64) = o2;
+}
+
+// cos / sin (first half) at position pos, columns d1 .. d1 + 3; the row is
+// clamped into the table (the host cannot see positions).
+__device__ __forceinline__ void rope_rows(const PrefillParams& p, int pos, int d1, half4_t& c, half4_t& s) {
+  const long row = min(max(pos, 0), p.rope_len - 1);
+  c = *reinterpret_cast<const half4_t*>(p.cos + row * p.rope_stride + d1);
+  s = *reinterpret_cast<const half4_t*>(p.sin + row * p.rope_stride + d1);
 }
 
 template <int KK, int KV>
@@ -181,32 +183,55 @@ __global__ __launch_bounds__(kThreads) void prefill_kernel(PrefillParams p) {
         for (int c = 0; c < KC; ++c) ak[u][c] = *reinterpret_cast<const half8_t*>(row + 32 * c + 8 * g);
       }
     }
-    const int ntiles = t.block_size / kKT;
-    for (int tt = 0; tt < ntiles; ++tt) {
-      const int tok0 = tt * kKT;
-      if (start + tok0 > qmax) break;  // later tiles of this block are after every query
-      // ---- reconstruct this wave's d tiles of K^T for tokens tok0 .. tok0 + 15
+    // tiles that hold a key at or before the last query of the workgroup
+    const int ntl = min(t.block_size / kKT, (qmax - start) / kKT + 1);
+    // Global inputs of one tile, loaded a tile ahead of their use.
+    struct TileIn {
+      uint2 ck[KC];   // K codes of token tok0 + n (KK = 16: 4 bytes in .x)
+      float scl;      // its K scale
+      half4_t c, s;   // cos / sin (first half) at its position, columns d1 .. d1 + 3
+      uint32_t cv[NTV];  // V codes of tokens tok0 + 4g .. +3, rank 16 nt + n
+      float4_t sv4;   // V scales of those tokens
+    };
+    const int d1 = 16 * w + 4 * g;
+    auto load_in = [&](int tok0, TileIn& in) __attribute__((always_inline)) {
       const int tok = tok0 + n;
-      const float scl = per_row ? sk[tok] : sk[0];
+      if constexpr (KK == 16) {
+        in.ck[0].x = *reinterpret_cast<const uint32_t*>(ck + (long)tok * KK + 4 * g);
+      } else {
+#pragma unroll
+        for (int c = 0; c < KC; ++c) in.ck[c] = *reinterpret_cast<const uint2*>(ck + (long)tok * KK + 32 * c + 8 * g);
+      }
+      in.scl = per_row ? sk[tok] : sk[0];
+      rope_rows(p, start + tok, d1, in.c, in.s);
+#pragma unroll
+      for (int nt = 0; nt < NTV; ++nt)
+        in.cv[nt] = *reinterpret_cast<const uint32_t*>(cv + (long)(16 * nt + n) * t.block_size + tok0 + 4 * g);
+      in.sv4 = per_row ? *reinterpret_cast<const float4_t*>(svp + tok0 + 4 * g) : (float4_t)svp[0];
+    };
+    TileIn cur, nxt;
+    load_in(0, cur);
+    for (int tt = 0; tt < ntl; ++tt) {
+      const int tok0 = tt * kKT;
+      if (tt + 1 < ntl) load_in(tok0 + kKT, nxt);
+      // ---- reconstruct this wave's d tiles of K^T for tokens tok0 .. tok0 + 15
       float4_t x[2];
 #pragma unroll
       for (int u = 0; u < 2; ++u) x[u] = (float4_t)0.f;
       if constexpr (KK == 16) {
-        const uint32_t cw = *reinterpret_cast<const uint32_t*>(ck + (long)tok * KK + 4 * g);
         half4_t cf;
 #pragma unroll
-        for (int e = 0; e < 4; ++e) cf[e] = (h16)((float)(int8_t)(cw >> (8 * e)) * scl);
+        for (int e = 0; e < 4; ++e) cf[e] = (h16)((float)(int8_t)(cur.ck[0].x >> (8 * e)) * cur.scl);
 #pragma unroll
         for (int u = 0; u < 2; ++u) x[u] = mfma_16x16x16(ak4[u], cf, x[u]);
       } else {
 #pragma unroll
         for (int c = 0; c < KC; ++c) {
-          const uint2 cw = *reinterpret_cast<const uint2*>(ck + (long)tok * KK + 32 * c + 8 * g);
           half8_t cf;
 #pragma unroll
           for (int e = 0; e < 4; ++e) {
-            cf[e] = (h16)((float)(int8_t)(cw.x >> (8 * e)) * scl);
-            cf[4 + e] = (h16)((float)(int8_t)(cw.y >> (8 * e)) * scl);
+            cf[e] = (h16)((float)(int8_t)(cur.ck[c].x >> (8 * e)) * cur.scl);
+            cf[4 + e] = (h16)((float)(int8_t)(cur.ck[c].y >> (8 * e)) * cur.scl);
           }
 #pragma unroll
           for (int u = 0; u < 2; ++u) x[u] = mfma_16x16x32(ak[u][c], cf, x[u]);
@@ -219,28 +244,22 @@ __global__ __launch_bounds__(kThreads) void prefill_kernel(PrefillParams p) {
         x1[e] = (h16)x[0][e];
         x2[e] = (h16)x[1][e];
       }
-      rope_store(p, x1, x2, start + tok, true, 16 * w + 4 * g, kbuf[buf] + n * kPitch);
+      rope_rotate_store(x1, x2, cur.c, cur.s, d1, kbuf[buf] + n * kPitch);
       __syncthreads();
       int kpos[4];
 #pragma unroll
       for (int e = 0; e < 4; ++e) kpos[e] = start + tok0 + 4 * g + e;
       const half4_t pp = scores(kpos);
       // ---- values in rank space: O_k^T[16 nt + n][q] += C_V[tok 4g + e][16 nt + n] * P[tok][q]
-      float4_t sv4;
-      if (per_row) {
-        sv4 = *reinterpret_cast<const float4_t*>(svp + tok0 + 4 * g);
-      } else {
-        sv4 = (float4_t)svp[0];
-      }
 #pragma unroll
       for (int nt = 0; nt < NTV; ++nt) {
-        const uint32_t cw = *reinterpret_cast<const uint32_t*>(cv + (long)(16 * nt + n) * t.block_size + tok0 + 4 * g);
         half4_t a;
 #pragma unroll
-        for (int e = 0; e < 4; ++e) a[e] = (h16)((float)(int8_t)(cw >> (8 * e)) * sv4[e]);
+        for (int e = 0; e < 4; ++e) a[e] = (h16)((float)(int8_t)(cur.cv[nt] >> (8 * e)) * cur.sv4[e]);
         ok[nt] = mfma_16x16x16(a, pp, ok[nt]);
       }
       buf ^= 1;
+      cur = nxt;
     }
     // ---- projection of the block: O_d^T[d][q] += B_V[d][k] O_k^T[k][q] (hi + lo fp16 parts)
     half4_t ph[NTV], pl[NTV];
@@ -269,31 +288,42 @@ __global__ __launch_bounds__(kThreads) void prefill_kernel(PrefillParams p) {
   const h16* tk = (const h16*)t.tail_k + ((long)b * t.kv_heads + h) * t.tail_capacity * 128;
   const h16* tv = (const h16*)t.tail_v + ((long)b * t.kv_heads + h) * t.tail_capacity * 128;
   const int32_t* tp = t.tail_pos + (long)b * t.tail_capacity;
-  for (int tok0 = 0; tok0 < tl; tok0 += kKT) {
-    // lane (g, n): token tok0 + n, d chunk d1 = 16 w + 4 g (and d1 + 64) of K and V
+  // Global inputs of one tail tile, loaded a tile ahead of their use: lane
+  // (g, n) takes token tok0 + n, columns d1 .. d1 + 3 and d1 + 64 .. of K
+  // and V, and the positions of tokens tok0 + 4g .. +3 (the mask).
+  struct TailIn {
+    half4_t x1, x2, v1, v2, c, s;
+    int kpos[4];
+  };
+  const int td1 = 16 * w + 4 * g;
+  auto load_tail = [&](int tok0, TailIn& in) __attribute__((always_inline)) {
     const int i = tok0 + n;
     const bool valid = i < tl;
     const int slot = valid ? (thead + i) % t.tail_capacity : 0;
-    const int pos = valid ? tp[slot] : -1;
-    const int d1 = 16 * w + 4 * g;
-    half4_t x1 = (half4_t)(h16)0, x2 = x1, v1 = x1, v2 = x1;
+    const half4_t z = (half4_t)(h16)0;
+    in.x1 = in.x2 = in.v1 = in.v2 = in.c = in.s = z;
     if (valid) {
-      x1 = *reinterpret_cast<const half4_t*>(tk + (long)slot * 128 + d1);
-      x2 = *reinterpret_cast<const half4_t*>(tk + (long)slot * 128 + d1 + 64);
-      v1 = *reinterpret_cast<const half4_t*>(tv + (long)slot * 128 + d1);
-      v2 = *reinterpret_cast<const half4_t*>(tv + (long)slot * 128 + d1 + 64);
+      in.x1 = *reinterpret_cast<const half4_t*>(tk + (long)slot * 128 + td1);
+      in.x2 = *reinterpret_cast<const half4_t*>(tk + (long)slot * 128 + td1 + 64);
+      in.v1 = *reinterpret_cast<const half4_t*>(tv + (long)slot * 128 + td1);
+      in.v2 = *reinterpret_cast<const half4_t*>(tv + (long)slot * 128 + td1 + 64);
+      rope_rows(p, tp[slot], td1, in.c, in.s);
     }
-    rope_store(p, x1, x2, pos, valid, d1, kbuf[buf] + n * kPitch);
-    *reinterpret_cast<half4_t*>(vbuf[buf] + n * kPitch + d1) = v1;
-    *reinterpret_cast<half4_t*>(vbuf[buf] + n * kPitch + d1 + 64) = v2;
-    __syncthreads();
-    int kpos[4];
 #pragma unroll
     for (int e = 0; e < 4; ++e) {
       const int ii = tok0 + 4 * g + e;
-      kpos[e] = ii < tl ? tp[(thead + ii) % t.tail_capacity] : -1;
+      in.kpos[e] = ii < tl ? tp[(thead + ii) % t.tail_capacity] : -1;
     }
-    const half4_t pp = scores(kpos);
+  };
+  TailIn tcur, tnxt;
+  if (tl > 0) load_tail(0, tcur);
+  for (int tok0 = 0; tok0 < tl; tok0 += kKT) {
+    if (tok0 + kKT < tl) load_tail(tok0 + kKT, tnxt);
+    rope_rotate_store(tcur.x1, tcur.x2, tcur.c, tcur.s, td1, kbuf[buf] + n * kPitch);
+    *reinterpret_cast<half4_t*>(vbuf[buf] + n * kPitch + td1) = tcur.v1;
+    *reinterpret_cast<half4_t*>(vbuf[buf] + n * kPitch + td1 + 64) = tcur.v2;
+    __syncthreads();
+    const half4_t pp = scores(tcur.kpos);
     // O_d^T[16 mt + n][q] += V[tok 4g + e][16 mt + n] P[tok][q]; V^T by transposing reads:
     // lane L of group g addresses row 4g + (L >> 2), columns 16 mt + 4 (L & 3)
 #pragma unroll
@@ -303,6 +333,7 @@ __global__ __launch_bounds__(kThreads) void prefill_kernel(PrefillParams p) {
       od[mt] = mfma_16x16x16(__builtin_bit_cast(half4_t, r), pp, od[mt]);
     }
     buf ^= 1;
+    tcur = tnxt;
   }
 
   // ---------------------------------------------------------------- output
