@@ -446,6 +446,31 @@ def model_loop(torch, device, prompt, decode_steps, layers=32):
     prefill_s, spec_s = spectral_run(prompt, decode_steps)
     log(f"spectral cache: {spec_s / decode_steps * 1e3:.2f} ms per token, prefill {prefill_s:.2f} s")
     st = get_cache_stats(model)
+    # decode attention of one token over every layer's final cache (HIP events)
+    from unsloth_spectral import _lib
+    from unsloth_spectral._decode import run_decode
+    hip = Hip()
+    stream = ctypes.c_void_p(torch.cuda.current_stream().cuda_stream)
+    g = torch.Generator(device=device)
+    g.manual_seed(14)
+    q1 = torch.randn(1, 32, 1, 128, generator=g, device=device).half()
+    calls = []
+    for layer in model.model.layers:
+        attn = layer.self_attn
+        c = attn._spectral_cache
+        cos, sin = attn._spectral_rope.get(c.current_position + 1, device)
+        calls.append((c, cos, sin, c.current_position - 1))
+    for c, cos, sin, qp in calls:
+        run_decode(q1, c, cos, sin, qp, rope_mode=_lib.SC_ROPE_ABSOLUTE, halves_equal=True)
+    torch.cuda.synchronize()
+    e0, e1 = hip.event(), hip.event()
+    reps = 20
+    hip.record(e0, stream)
+    for _ in range(reps):
+        for c, cos, sin, qp in calls:
+            run_decode(q1, c, cos, sin, qp, rope_mode=_lib.SC_ROPE_ABSOLUTE, halves_equal=True)
+    hip.record(e1, stream)
+    attn_ms = hip.elapsed_ms(e0, e1) / reps
     return {
         "metric": "model decode tokens/s (spectral cache vs dense fp16 KV cache)",
         "value": round(decode_steps / spec_s, 2), "unit": "tokens/s", "n_gpus": 1, "steps": decode_steps,
@@ -461,7 +486,9 @@ def model_loop(torch, device, prompt, decode_steps, layers=32):
                      "cold_blocks_per_layer": st["total_blocks"] // layers,
                      "compressions_during_decode": (prompt + decode_steps) // TB - prompt // TB,
                      "kv_bytes": st["total_compressed_bytes"], "kv_bytes_fp16": st["total_original_bytes"],
-                     "compression_ratio": round(st["compression_ratio"], 3)},
+                     "compression_ratio": round(st["compression_ratio"], 3),
+                     "attention_ms_per_token": round(attn_ms, 3),
+                     "attention_share": round(attn_ms / (spec_s / decode_steps * 1e3), 4)},
         "dense_fp16_kv": {"decode_ms_per_token": round(dense_s / decode_steps * 1e3, 3),
                           "tokens_per_s": round(decode_steps / dense_s, 2)},
         "model_init_s": round(init_s, 1),
