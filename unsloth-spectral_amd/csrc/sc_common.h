@@ -100,10 +100,13 @@ __device__ __forceinline__ half8_t i8x8_to_h8(uint2 w) {
   return (half8_t){a.x, a.y, a.z, a.w, b.x, b.y, b.z, b.w};
 }
 
-// Scheduling fence: the machine scheduler moves no instruction of any kind
-// across this point (mask 0).  Placed right after prefetch loads so that they
-// are issued where the source issues them, ahead of the compute they overlap.
-__device__ __forceinline__ void pin_vmem() { __builtin_amdgcn_sched_barrier(0); }
+// Scheduling fence for memory instructions: the machine scheduler moves no
+// load, store or LDS access across this point, while ALU, MFMA and
+// transcendental instructions may still cross it (sched_barrier mask 0x40F).
+// Placed right after prefetch loads so that they are issued where the
+// source issues them, ahead of the compute they overlap, without keeping
+// the surrounding arithmetic from interleaving.
+__device__ __forceinline__ void pin_vmem() { __builtin_amdgcn_sched_barrier(0x40F); }
 
 __device__ __forceinline__ half2_t pack_h2(float a, float b) {
   return (half2_t){(h16)a, (h16)b};

@@ -640,15 +640,28 @@ __device__ __forceinline__ void apply_rinv(float* Ys, int rows, const float* Xf)
   }
 }
 
-// Players p < q of round-robin pair m at `step` (P players, P even; pair m
-// is slots m and P-1-m of a circle whose player 0 stays put).
-__device__ __forceinline__ void jacobi_players(int P, int m, int step, int& pp, int& qq) {
-  const int i1 = m, i2 = P - 1 - m;
-  const int a = i1 == 0 ? 0 : 1 + (i1 - 1 + step) % (P - 1);
-  const int b = 1 + (i2 - 1 + step) % (P - 1);
-  pp = a < b ? a : b;
-  qq = a < b ? b : a;
-}
+// Players p < q of round-robin pair m (P players, P even), advanced one
+// round at a time without division: player 0 sits at circle position 0,
+// the others occupy positions 1..P-1 and move one position per round
+// (wrapping over the P - 1 moving slots); pair m is positions m and
+// P - 1 - m.
+struct PairWalk {
+  int a, b, wrap;  // moving-slot indices (a < 0: fixed player 0); wrap = P - 1
+  __device__ __forceinline__ void start(int P, int m) {
+    wrap = P - 1;
+    a = m == 0 ? -1 : m - 1;
+    b = P - 2 - m;
+  }
+  __device__ __forceinline__ void players(int& pp, int& qq) const {
+    const int x = a < 0 ? 0 : a + 1, y = b + 1;
+    pp = x < y ? x : y;
+    qq = x < y ? y : x;
+  }
+  __device__ __forceinline__ void next() {
+    if (a >= 0) a = a + 1 == wrap ? 0 : a + 1;
+    b = b + 1 == wrap ? 0 : b + 1;
+  }
+};
 
 // Jacobi rotation (c, s) that zeroes G[p][q]: tau in fp64 (scale-free), the
 // angle in fp32, then (c, s) renormalised in fp64 by one Newton step, so
@@ -679,10 +692,13 @@ __device__ __forceinline__ void jacobi_rotation(double app, double aqq, double a
 //   2. thread i < NB rotates the 2x2 block (pair mi, pair mk), mi <= mk, of
 //      Gs from both sides (Gs <- J^T Gs J) and writes its mirror; thread t
 //      rotates rows t / NP, t / NP + cnt, ... of pair t % NP of Ws from the
-//      right (cnt = number of threads with that pair).  Pair players are
-//      recomputed arithmetically, so the rotation and element reads go out
-//      together; each element has one owner, so the updates are in place.
-// Stops when the off-diagonal mass is <= 1e-24 of the diagonal mass.
+//      right (cnt = number of threads with that pair).  Each thread walks
+//      the players of its pairs with PairWalk counters, so the rotation and
+//      element reads go out together; each element has one owner, so the
+//      updates are in place.
+// Stops when the off-diagonal mass is <= 1e-16 of the diagonal mass (the
+// off-diagonal norm below 1e-8 of the diagonal's, far below the fp32 and
+// INT8 rounding of the outputs).
 // scratch: >= 2 * RM / 2 + 2 * kThreads / 64 doubles.
 template <int RM>
 __device__ __forceinline__ void jacobi_eig(double* Gs, double* Ws, double* scratch, int r) {
@@ -735,11 +751,16 @@ __device__ __forceinline__ void jacobi_eig(double* Gs, double* Ws, double* scrat
       off += part[2 * w];
       dia += part[2 * w + 1];
     }
-    if (off <= 1e-24 * dia || dia == 0.0) break;  // off-diagonal norm below 1e-12 of the diagonal
-    for (int step = 0; step < P - 1; ++step) {
+    if (off <= 1e-16 * dia || dia == 0.0) break;
+    PairWalk wt, wi, wk, wv;
+    wt.start(P, t < NPr ? t : 0);
+    wi.start(P, mi);
+    wk.start(P, mk);
+    wv.start(P, mv);
+    for (int step = 0; step < P - 1; ++step, wt.next(), wi.next(), wk.next(), wv.next()) {
       if (t < NPr) {
         int pp, qq;
-        jacobi_players(P, t, step, pp, qq);
+        wt.players(pp, qq);
         double c, sn;
         jacobi_rotation(Gs[pp * RM + pp], Gs[qq * RM + qq], Gs[pp * RM + qq], c, sn);
         rot[2 * t] = c;
@@ -748,8 +769,8 @@ __device__ __forceinline__ void jacobi_eig(double* Gs, double* Ws, double* scrat
       __syncthreads();
       if (t < NBr) {
         int pi, qi, pk, qk;
-        jacobi_players(P, mi, step, pi, qi);
-        jacobi_players(P, mk, step, pk, qk);
+        wi.players(pi, qi);
+        wk.players(pk, qk);
         const double ci = rot[2 * mi], si = rot[2 * mi + 1], ck = rot[2 * mk], sk = rot[2 * mk + 1];
         const double a00 = Gs[pi * RM + pk], a01 = Gs[pi * RM + qk];
         const double a10 = Gs[qi * RM + pk], a11 = Gs[qi * RM + qk];
@@ -770,7 +791,7 @@ __device__ __forceinline__ void jacobi_eig(double* Gs, double* Ws, double* scrat
       }
       {
         int pm, qm;
-        jacobi_players(P, mv, step, pm, qm);
+        wv.players(pm, qm);
         const double cm = rot[2 * mv], sm = rot[2 * mv + 1];
         for (int c = t / NPr; c < P; c += vcnt) {
           const double vp = Ws[c * RM + pm], vq = Ws[c * RM + qm];
