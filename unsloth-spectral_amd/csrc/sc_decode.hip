@@ -52,7 +52,6 @@ constexpr long kFillUnits = 512;  // two resident workgroups per CU on 256 CUs
 // once it has finished this many ranges, which evens out the finish times.
 constexpr int kYoungPrioRange = 2;
 constexpr int kVRow = 132;                              // LDS row (halves) of a staged V tile
-constexpr int kCombineWaves = 4;  // waves (query heads) per combine workgroup
 constexpr float kLog2e = 1.4426950408889634f;
 
 struct DecodeParams {
@@ -1117,16 +1116,19 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(2))) v
 }
 
 // Log-sum-exp merge of the partial records of one (sequence, query head):
-// one wave per query head, lane l owns d = E l .. E l + E - 1.  The records
-// of U units are loaded together (m and l are wave-uniform broadcasts), then
-// folded in registers.
+// one single-wave workgroup per query head, lane l owns d = E l .. E l + E - 1.
+// Records are merged U at a time with every load of a chunk in flight at
+// once: lane k (and k + U) loads the (m, l) header of record k, the chunk
+// maximum and the weighted sum of l are lane reductions, and the weight of
+// record k reaches every lane by readlane (an SGPR operand of the FMAs).
+// Every unit writes its record (m = -inf, l = 0, o = 0 when it saw no
+// token), so a weight of zero needs no branch.
 template <int D>
-__global__ __launch_bounds__(64 * kCombineWaves) void decode_combine_kernel(DecodeParams p) {
+__global__ __launch_bounds__(64) void decode_combine_kernel(DecodeParams p) {
   constexpr int PREC = Geo<D>::PREC;
   constexpr int E = D / 64;  // d values per lane
-  constexpr int U = 16;      // records in flight per wave
-  const int wq = blockIdx.x * kCombineWaves + (threadIdx.x >> 6);
-  if (wq >= p.B * p.Hq) return;
+  constexpr int U = 32;      // records per chunk (lanes k and k + 32 hold header k)
+  const int wq = blockIdx.x;
   const int b = wq / p.Hq, qh = wq % p.Hq;
   const int h = qh / p.nrep, hh = qh % p.nrep;
   const int lane = threadIdx.x & 63;
@@ -1137,25 +1139,47 @@ __global__ __launch_bounds__(64 * kCombineWaves) void decode_combine_kernel(Deco
 #pragma unroll
   for (int e = 0; e < E; ++e) O[e] = 0.f;
   for (int u0 = 0; u0 < W; u0 += U) {
-    float mr[U], lr[U], orr[U][E];
+    const int ku = u0 + (lane & (U - 1));
+    const bool has = ku < W;
+    const float* rh = r0 + (long)(has ? ku : u0) * us;
+    const float2 ml = *reinterpret_cast<const float2*>(rh);
+    float orr[U][E];
 #pragma unroll
     for (int k = 0; k < U; ++k) {
-      const float* r = r0 + (long)min(u0 + k, W - 1) * us;
-      mr[k] = u0 + k < W ? r[0] : -INFINITY;
-      lr[k] = r[1];
+      const float* r = r0 + (long)min(u0 + k, W - 1) * us + 4 + E * lane;
+      if constexpr (E == 2) {
+        const float2 v = *reinterpret_cast<const float2*>(r);
+        orr[k][0] = v.x;
+        orr[k][1] = v.y;
+      } else {
 #pragma unroll
-      for (int e = 0; e < E; ++e) orr[k][e] = r[4 + E * lane + e];
+        for (int e = 0; e < E; ++e) orr[k][e] = r[e];
+      }
     }
+    // Keep every load of the chunk above the reductions: left alone, the
+    // scheduler sinks them to their uses and the chunk costs two round trips.
+    __builtin_amdgcn_sched_barrier(0);
+    const float mk = has ? ml.x : -INFINITY;
+    float mc = mk;
+#pragma unroll
+    for (int o = U / 2; o > 0; o >>= 1) mc = fmaxf(mc, __shfl_xor(mc, o));
+    const float mn = fmaxf(M, mc);
+    if (mn == -INFINITY) continue;  // wave-uniform: nothing seen yet
+    const float ck = mk == -INFINITY ? 0.f : fast_exp2(mk - mn);
+    float lc = has ? ml.y * ck : 0.f;
+#pragma unroll
+    for (int o = U / 2; o > 0; o >>= 1) lc += __shfl_xor(lc, o);
+    const float a = fast_exp2(M - mn);  // exp2(-inf) = 0 on the first chunk
+    L = L * a + lc;
+#pragma unroll
+    for (int e = 0; e < E; ++e) O[e] *= a;
 #pragma unroll
     for (int k = 0; k < U; ++k) {
-      if (mr[k] == -INFINITY) continue;
-      const float mn = fmaxf(M, mr[k]);
-      const float a = fast_exp2(M - mn), c = fast_exp2(mr[k] - mn);
-      L = L * a + lr[k] * c;
+      const float c = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(ck), k));
 #pragma unroll
-      for (int e = 0; e < E; ++e) O[e] = O[e] * a + orr[k][e] * c;
-      M = mn;
+      for (int e = 0; e < E; ++e) O[e] = __builtin_fmaf(orr[k][e], c, O[e]);
     }
+    M = mn;
   }
   h16* o = p.out + b * p.out_sb + (long)qh * p.out_sh + E * lane;
 #pragma unroll
@@ -1315,8 +1339,7 @@ int launch(DecodeParams& p, hipStream_t s) {
     int rc = sc_launch_status("decode_partial_kernel");
     if (rc) return rc;
   }
-  const int cgrid = (p.B * p.Hq + kCombineWaves - 1) / kCombineWaves;
-  hipLaunchKernelGGL((decode_combine_kernel<D>), dim3(cgrid), dim3(64 * kCombineWaves), 0, s, p);
+  hipLaunchKernelGGL((decode_combine_kernel<D>), dim3(p.B * p.Hq), dim3(64), 0, s, p);
   return sc_launch_status("decode_combine_kernel");
 }
 
