@@ -31,7 +31,7 @@
 extern "C" {
 #endif
 
-#define SC_ABI_VERSION 4
+#define SC_ABI_VERSION 5
 
 #define SC_OK 0
 #define SC_ERR_INVALID (-1)      /* bad argument / shape */
@@ -176,6 +176,14 @@ int sc_decode_attn(const ScDecodeArgs* args, void* workspace, size_t workspace_b
  *   basis  fp16 : basis_dmajor=1 -> [cols][kp], 0 -> [kp][cols]
  * Optional fp32 testing outputs (NULL = skipped): coeffs [count][rows][rank],
  * svals [count][rank], vh [count][rank][cols], omega_out [count][cols][r].
+ * row_weights (NULL = unweighted): fp32 [rows] per matrix, indexed like the
+ * outputs (row_weights + (i/inner)*stride_outer + (i%inner)*stride_inner; a
+ * stride of 0 shares one vector).  Attention-weighted compression
+ * (spectral_cache.py:351-393, `_compress_tensor` with attention_weights):
+ * w = sqrt(a / mean(a)), the SVD runs on diag(w) M (products in fp32 on the
+ * VALU for every input type), and the coefficients are divided by w before
+ * quantisation.  Weights must be positive (a zero weight divides by zero,
+ * as in the reference).
  * Supported: rows <= 512 (multiple of 64), cols in {64, 128},
  * rank + oversample <= 40.
  */
@@ -206,6 +214,8 @@ typedef struct ScCompressArgs {
   float* svals_out;
   float* vh_out;
   float* omega_out;
+  const float* row_weights;
+  int64_t row_weights_stride_outer, row_weights_stride_inner;
 } ScCompressArgs;
 
 int sc_rsvd_compress(const ScCompressArgs* args, void* stream);

@@ -7,7 +7,8 @@ Reference: unsloth_spectral/spectral_cache.py
   * ``_compress_hot_cache``  :243-319  (while loop over full blocks,
                                         start_position = hot_position_ids[0,0])
   * ``_compress_tensor``     :321-407  (rSVD k, n_iter=2, p=5 -> coeffs=U*S ->
-                                        quantise -> fp16 casts)
+                                        quantise -> fp16 casts; attention-
+                                        weighted branch :351-368, :389-393)
   * ``get_spectral_components`` / ``get_all_positions`` / ``get_kv`` :518-612
 One sequence (the reference asserts batch 1, :346).  ``omega_fn(kind,
 block_index, shape)`` supplies the Gaussian sketch that the reference draws
@@ -20,18 +21,34 @@ from .quant import quantize_per_head, quantize_per_row
 from .rsvd import oversampled_rank, randomized_svd_ref, randomized_svd_subspace64
 
 
+def row_weights(attention_weights):
+    """spectral_cache.py:356-358: w = sqrt(a / mean(a)) in float32."""
+    a = np.asarray(attention_weights, np.float32).reshape(-1)
+    return np.sqrt(a / np.float32(a.mean(dtype=np.float32))).astype(np.float32)
+
+
 def compress_tensor(X, rank, omega, granularity="per_head", n_iter=2, oversampling=5,
-                    algorithm="reference"):
+                    algorithm="reference", attention_weights=None):
     """spectral_cache.py:321-407 for X [H, T, D] (any float dtype).
+
+    ``attention_weights`` [T] selects the attention-weighted branch
+    (:351-368, :389-393): the SVD runs on X * w (w per token row) and the
+    coefficients are divided by w before quantisation.
 
     Returns (codes int8 [H,T,k], scale f32 [H] or [H,T], basis f16 [H,k,D],
     minmax f32 [H,2], coeffs f32 [H,T,k] before quantisation)."""
     Xf = np.asarray(X, np.float32)                      # .float(), :349
+    w = None
+    if attention_weights is not None:
+        w = row_weights(attention_weights)
+        Xf = (Xf * w[None, :, None]).astype(np.float32)  # :361-362
     if algorithm == "reference":
         U, S, Vh = randomized_svd_ref(Xf, rank, omega, n_iter, oversampling)
     else:
         U, S, Vh = randomized_svd_subspace64(Xf, rank, omega, n_iter, oversampling)
     coeffs = (np.asarray(U, np.float32) * np.asarray(S, np.float32)[:, None, :]).astype(np.float32)  # :387
+    if w is not None:
+        coeffs = (coeffs / w[None, :, None]).astype(np.float32)          # :391-393
     if granularity == "per_head":
         codes, scale, _, minmax = quantize_per_head(coeffs)            # :398
     else:

@@ -36,7 +36,7 @@ def test_library_exports_every_declared_symbol():
     for fn in _declared_functions():
         assert hasattr(lib, fn), fn
     assert set(_lib.PROTOTYPES) == _declared_functions()
-    assert _lib.load().sc_abi_version() == _lib.ABI_VERSION == 4
+    assert _lib.load().sc_abi_version() == _lib.ABI_VERSION == 5
 
 
 def test_struct_layouts_match_header():

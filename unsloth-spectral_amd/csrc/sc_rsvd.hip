@@ -49,6 +49,8 @@ struct RsvdParams {
   float* svals_out;
   float* vh_out;
   float* omega_out;
+  const float* row_weights;
+  long rw_so, rw_si;
   // tier mode
   int tier_mode;
   int B, Hkv, NB, TCAP, max_new;
@@ -71,7 +73,13 @@ struct Job {
   h16* basis;
   unsigned long long stream;
   long index;  // generic matrix index (debug outputs), -1 in tier mode
+  const float* rw;  // row importances a[rows] (weighted compression) or nullptr
+  float rw_mean;    // mean(a)
 };
+
+// Row weight of attention-weighted compression, sqrt(a / mean(a)) with IEEE
+// division and square root (spectral_cache.py:356-358).
+__device__ __forceinline__ float row_weight(const Job& j, int row) { return sqrtf(j.rw[row] / j.rw_mean); }
 
 __device__ __forceinline__ const char* row_ptr(const Job& j, int t, int cols) {
   if (j.ring_cap > 0) return j.src + (long)((j.ring_head + t) % j.ring_cap) * cols * j.esize;
@@ -179,6 +187,8 @@ __device__ __forceinline__ void gemm_rows(const Job& j, int rows, int cols, cons
   const bool v0 = t < rows, v1 = t + kThreads < rows;
   const char* r0 = v0 ? row_ptr(j, t, cols) : nullptr;
   const char* r1 = v1 ? row_ptr(j, t + kThreads, cols) : nullptr;
+  // weighted rows: (w M)[row][d] rounded to fp32 once, as X * W (spectral_cache.py:361-362)
+  const float w0 = j.rw && v0 ? row_weight(j, t) : 1.f, w1 = j.rw && v1 ? row_weight(j, t + kThreads) : 1.f;
   for (int d0 = 0; d0 < cols; d0 += 8) {
     float m0[8], m1[8];
     if (v0) load8(r0 + (long)d0 * j.esize, j.dtype, m0);
@@ -191,7 +201,7 @@ __device__ __forceinline__ void gemm_rows(const Job& j, int rows, int cols, cons
       for (int dd = 0; dd < 8; ++dd) m1[dd] = 0.f;
 #pragma unroll
     for (int dd = 0; dd < 8; ++dd) {
-      const float a0 = m0[dd], a1 = m1[dd];
+      const float a0 = m0[dd] * w0, a1 = m1[dd] * w1;
       const float* z = Zs + (d0 + dd) * RM;
 #pragma unroll
       for (int c = 0; c < RM; ++c) {
@@ -227,7 +237,8 @@ __device__ __forceinline__ void gemm_cols(const Job& j, int rows, int cols, cons
 #pragma unroll
   for (int c = 0; c < CW2; ++c) z[c] = 0.f;
   for (int row = 0; row < rows; ++row) {
-    const float mv = load1(row_ptr(j, row, cols) + (long)d * j.esize, j.dtype);
+    float mv = load1(row_ptr(j, row, cols) + (long)d * j.esize, j.dtype);
+    if (j.rw) mv *= row_weight(j, row);
     const float* y = Ys + row * RM + c0;
 #pragma unroll
     for (int c = 0; c < CW2; ++c)
@@ -827,7 +838,7 @@ __device__ __forceinline__ void run_matrix(const RsvdParams& p, const Job& j, in
   if (p.omega_out && dbg_index >= 0)
     for (int e = t; e < cols * r; e += kThreads) p.omega_out[dbg_index * cols * r + e] = L.Zs[(e / r) * RM + e % r];
 
-  const bool mf = j.dtype == SC_DTYPE_F16;  // MFMA products (fp16 input); else fp32 VALU
+  const bool mf = j.dtype == SC_DTYPE_F16 && !j.rw;  // MFMA products (fp16 input, unweighted); else fp32 VALU
   auto mul_m = [&]() __attribute__((always_inline)) {  // Ys = M Zs
     if (mf) {
       gemm_rows_mfma<RM>(j, rows, cols, L.Zs, L.Ys);
@@ -914,6 +925,15 @@ __device__ __forceinline__ void run_matrix(const RsvdParams& p, const Job& j, in
         cf1[i + 3] = fmaf(q1, w.w, cf1[i + 3]);
       }
     }
+  }
+  if (j.rw) {  // undo the row weighting: coeffs / W (spectral_cache.py:389-393)
+    const float w0 = v0 ? row_weight(j, t) : 1.f, w1 = v1 ? row_weight(j, t + kThreads) : 1.f;
+#pragma unroll
+    for (int i = 0; i < RM; ++i)
+      if (i < k) {
+        cf0[i] = cf0[i] / w0;
+        cf1[i] = cf1[i] / w1;
+      }
   }
   __syncthreads();  // Q no longer needed: Ys is reused for Vh
   // Vh (unnormalised) into Ys as [k][cols]: Vh_i[d] = sum_c W[c][ord_i] Bp^T[d][c].
@@ -1084,6 +1104,20 @@ __global__ __launch_bounds__(kThreads) void rsvd_generic_kernel(RsvdParams p) {
   j.basis = p.basis + io * p.bs_so + ii * p.bs_si;
   j.stream = (unsigned long long)i;
   j.index = i;
+  j.rw = nullptr;
+  j.rw_mean = 1.f;
+  if (p.row_weights) {  // mean of the row importances (spectral_cache.py:357), one block reduction
+    j.rw = p.row_weights + io * p.rw_so + ii * p.rw_si;
+    const int t = threadIdx.x;
+    float s = 0.f;
+    for (int e = t; e < p.rows; e += kThreads) s += j.rw[e];
+    s = wave_sum(s);
+    float* fr = reinterpret_cast<float*>(L.red);
+    if ((t & 63) == 0) fr[t >> 6] = s;
+    __syncthreads();
+    j.rw_mean = ((fr[0] + fr[1]) + (fr[2] + fr[3])) / (float)p.rows;
+    __syncthreads();
+  }
   run_matrix<RM>(p, j, p.rows, p.cols, p.n_iter, L, p.omega ? p.omega + i * (long)p.cols * p.r : nullptr, i);
 }
 
@@ -1115,6 +1149,8 @@ __global__ __launch_bounds__(kThreads) void rsvd_tier_kernel(RsvdParams p) {
   Job j;
   j.dtype = SC_DTYPE_F16;
   j.esize = 2;
+  j.rw = nullptr;
+  j.rw_mean = 1.f;
   j.src = (const char*)((const h16*)(kind ? T.tail_v : T.tail_k) + bh * p.TCAP * D);
   j.row_stride = D;
   j.ring_head = head;
@@ -1215,6 +1251,9 @@ extern "C" int sc_rsvd_compress(const ScCompressArgs* a, void* stream) {
   p.svals_out = a->svals_out;
   p.vh_out = a->vh_out;
   p.omega_out = a->omega_out;
+  p.row_weights = a->row_weights;
+  p.rw_so = a->row_weights_stride_outer;
+  p.rw_si = a->row_weights_stride_inner;
   hipStream_t s = (hipStream_t)stream;
   int rc;
   if (rm == 24) {

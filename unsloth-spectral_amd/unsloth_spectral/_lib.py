@@ -12,7 +12,7 @@ import torch
 _HERE = os.path.dirname(os.path.abspath(__file__))
 LIB_PATH = os.path.join(_HERE, "libspectral_hip.so")
 
-ABI_VERSION = 4  # SC_ABI_VERSION of include/spectral_hip.h
+ABI_VERSION = 5  # SC_ABI_VERSION of include/spectral_hip.h
 SC_OK = 0
 SC_ROPE_ABSOLUTE, SC_ROPE_DISTANCE, SC_ROPE_NONE = 0, 1, 2
 SC_QUANT_PER_HEAD, SC_QUANT_PER_ROW, SC_QUANT_PER_TENSOR = 0, 1, 2
@@ -77,6 +77,7 @@ class ScCompressArgs(ctypes.Structure):
         ("vnorm", c_vp), ("vnorm_stride_outer", c_i64), ("vnorm_stride_inner", c_i64),
         ("basis", c_vp), ("basis_stride_outer", c_i64), ("basis_stride_inner", c_i64),
         ("coeffs_out", c_vp), ("svals_out", c_vp), ("vh_out", c_vp), ("omega_out", c_vp),
+        ("row_weights", c_vp), ("row_weights_stride_outer", c_i64), ("row_weights_stride_inner", c_i64),
     ]
 
 

@@ -19,8 +19,13 @@ from ._lib import check, ptr
 
 def compress_matrices(M: torch.Tensor, k: int, n_iter: int = 2, oversampling: int = 5,
                       omega: Optional[torch.Tensor] = None, seed: int = 0, granularity: str = "per_head",
-                      coeff_major: bool = False, basis_dmajor: bool = False, debug: bool = False):
+                      coeff_major: bool = False, basis_dmajor: bool = False, debug: bool = False,
+                      row_weights: Optional[torch.Tensor] = None):
     """Compresses M [N, m, n] into INT8 codes + scales + fp16 basis.
+
+    ``row_weights`` ([m] shared by every matrix, or [N, m]; positive) selects
+    attention-weighted compression (spectral_cache.py:351-393): the SVD of
+    diag(w) M with w = sqrt(a / mean(a)), coefficients divided by w.
 
     Returns a dict with ``codes`` (int8 [N, m, kp] or [N, kp, m]), ``scales``
     (f32 [N] or [N, m]), ``minmax`` [N, 2], ``vnorm`` [N], ``basis`` (f16
@@ -77,6 +82,16 @@ def compress_matrices(M: torch.Tensor, k: int, n_iter: int = 2, oversampling: in
         a.svals_out = dbg["svals"].data_ptr()
         a.vh_out = dbg["vh"].data_ptr()
         a.omega_out = dbg["omega"].data_ptr()
+    rw = None
+    if row_weights is not None:
+        rw = row_weights.to(device=dev, dtype=torch.float32).contiguous()
+        if rw.shape == (m,):
+            a.row_weights_stride_outer = 0
+        elif rw.shape == (N, m):
+            a.row_weights_stride_outer = m
+        else:
+            raise ValueError(f"row_weights must be [{m}] or [{N}, {m}], got {tuple(rw.shape)}")
+        a.row_weights = rw.data_ptr()
     check(_lib.load().sc_rsvd_compress(ctypes.byref(a), _lib.stream_of(Mc)))
     out = {"codes": codes, "scales": scales, "minmax": minmax, "vnorm": vnorm, "basis": basis,
            "kp": kp, "r": r}

@@ -65,8 +65,13 @@ class SpectralCache:
       quant_granularity "per_head" (reference) or "per_row"
       oversampling, n_iter   rSVD parameters (rsvd.py defaults 5, 2)
       seed              seed of the on-device Gaussian sketch
-    ``hot_buffer_size``, ``use_attention_weighted_svd`` and landmarks are
-    stored but unused, as in the reference main path (:93, :100-101)."""
+    ``hot_buffer_size`` is stored but unused, as in the reference (:93).
+    ``use_attention_weighted_svd`` and landmarks behave as in the reference:
+    the block compression of ``append`` never passes attention weights
+    (:285-286), and landmark tokens enter only through ``add_landmarks``;
+    ``_compress_tensor``, ``update_attention_importance``,
+    ``get_block_attention_weights``, ``add_landmarks`` and
+    ``get_kv_with_landmarks`` are the reference's (:321-407, :710-852)."""
 
     def __init__(self, num_heads: int, head_dim: int, block_size: int = 512, k_rank_keys: int = 16,
                  k_rank_values: int = 32, hot_buffer_size: int = 64, device="cuda",
@@ -118,6 +123,10 @@ class SpectralCache:
 
     # ------------------------------------------------------------ storage
     def _zero_host(self):
+        self.attention_importance = None
+        self.landmark_K = None
+        self.landmark_V = None
+        self.landmark_position_ids = None
         self.total_tokens = 0
         self.current_position = 0
         self.compression_count = 0
@@ -372,6 +381,113 @@ class SpectralCache:
             parts_k.append(self.hot_K)
             parts_v.append(self.hot_V)
         return torch.cat(parts_k, dim=2), torch.cat(parts_v, dim=2)
+
+    # ------------------------------------------------------------ weighted SVD, landmarks
+    def _compress_tensor(self, X: torch.Tensor, rank: int, attention_weights: Optional[torch.Tensor] = None):
+        """spectral_cache.py:321-407: compresses X [1, H, T, D] on the device.
+
+        Returns (coeffs [H, T, rank] = dequantised INT8 codes in the cache
+        dtype, basis [H, rank, D] in the cache dtype, scales [H, 2] = per-head
+        (min, max) of the coefficients).  With ``use_attention_weighted_svd``
+        and ``attention_weights`` [T], rows are weighted by
+        sqrt(a / mean(a)) for the SVD and the coefficients unweighted
+        (:351-368, :389-393).  The Gaussian sketch is drawn on the device."""
+        from .rsvd import compress_matrices
+        _lib.require_device(X, "X")
+        B, H, T, D = X.shape
+        if B != 1:
+            raise ValueError("Batch size must be 1 for now")   # :346
+        M = X[0]
+        if M.dtype not in _lib.SC_DTYPE:
+            M = M.float()
+        w = None
+        if self.use_attention_weighted_svd and attention_weights is not None:
+            w = attention_weights.reshape(-1)
+            if w.numel() != T:
+                raise ValueError(f"attention_weights must hold {T} entries, got {w.numel()}")
+        seed = (self.seed * 0x9E3779B97F4A7C15 + self._compress_calls) & 0xFFFFFFFFFFFFFFFF
+        self._compress_calls += 1
+        res = compress_matrices(M, rank, self.n_iter, self.oversampling, seed=seed, granularity="per_head",
+                                row_weights=w)
+        kp_codes = res["codes"][:, :, :rank].float()
+        coeffs = (kp_codes * res["scales"][:, None, None]).to(self.dtype)
+        basis = res["basis"][:, :rank, :].to(self.dtype)
+        return coeffs, basis, res["minmax"]
+
+    def update_attention_importance(self, attention_weights: torch.Tensor, query_position: int):
+        """spectral_cache.py:710-750: running average (alpha 0.1) of the
+        attention probabilities [B, H, 1, T_kv] averaged over batch and
+        heads; no-op unless ``use_attention_weighted_svd``."""
+        if not self.use_attention_weighted_svd:
+            return
+        avg = attention_weights.mean(dim=(0, 1, 2))
+        if self.attention_importance is None:
+            self.attention_importance = avg.clone()
+            return
+        alpha = 0.1
+        if self.attention_importance.shape[0] < avg.shape[0]:
+            pad = torch.zeros(avg.shape[0] - self.attention_importance.shape[0], device=avg.device, dtype=avg.dtype)
+            self.attention_importance = torch.cat([self.attention_importance, pad])
+        n = avg.shape[0]
+        self.attention_importance[:n] = (1 - alpha) * self.attention_importance[:n] + alpha * avg
+
+    def get_block_attention_weights(self, block_idx: int) -> Optional[torch.Tensor]:
+        """spectral_cache.py:752-777: importance of block ``block_idx``'s
+        tokens, or None when not tracked that far."""
+        if self.attention_importance is None:
+            return None
+        start = block_idx * self.block_size
+        end = start + self.block_size
+        if end > self.attention_importance.shape[0]:
+            return None
+        return self.attention_importance[start:end]
+
+    def add_landmarks(self, K: torch.Tensor, V: torch.Tensor, position_ids: torch.Tensor):
+        """spectral_cache.py:779-802: FP16 tokens that are never compressed,
+        K, V [B, H, T, D], position_ids [B, T]; appended to earlier ones."""
+        _lib.require_device(K, "K")
+        if self.landmark_K is None:
+            self.landmark_K = K.clone()
+            self.landmark_V = V.clone()
+            self.landmark_position_ids = position_ids.clone()
+        else:
+            self.landmark_K = torch.cat([self.landmark_K, K], dim=2)
+            self.landmark_V = torch.cat([self.landmark_V, V], dim=2)
+            self.landmark_position_ids = torch.cat([self.landmark_position_ids, position_ids], dim=1)
+
+    def get_kv_with_landmarks(self):
+        """spectral_cache.py:804-852: (K, V, position_ids) with landmarks
+        first, then the reconstructed cold blocks, then the FP16 tail;
+        (None, None, None) when everything is empty."""
+        K_parts, V_parts, pos_parts = [], [], []
+        if self.landmark_K is not None:
+            K_parts.append(self.landmark_K)
+            V_parts.append(self.landmark_V)
+            if self.landmark_position_ids is not None:
+                pos_parts.append(self.landmark_position_ids)
+        if self._B is not None and self.total_tokens > 0 and self._n_cold:
+            shape = (self._B, self.num_heads, self._n_cold * self.block_size, self.head_dim)
+            k = torch.empty(shape, dtype=torch.float16, device=self.device)
+            v = torch.empty_like(k)
+            check(_lib.load().sc_tier_dequant(ctypes.byref(self._tier()), 0, self._n_cold, ptr(k), ptr(v),
+                                              _lib.stream_of(k)))
+            K_parts.append(k)
+            V_parts.append(v)
+            for s in self.block_start[0, :self._n_cold].tolist():
+                pos_parts.append(torch.arange(s, s + self.block_size, device=self.device).unsqueeze(0))
+        if self._B is not None and self.total_tokens > 0 and self._tail_len:
+            K_parts.append(self.hot_K)
+            V_parts.append(self.hot_V)
+            hp = self.hot_position_ids
+            if hp is not None:
+                pos_parts.append(hp)
+        if not K_parts:
+            return None, None, None
+        dt = K_parts[0].dtype
+        K_full = torch.cat([x.to(dt) for x in K_parts], dim=2)
+        V_full = torch.cat([x.to(dt) for x in V_parts], dim=2)
+        pos = torch.cat([p_.to(torch.long) for p_ in pos_parts], dim=1) if pos_parts else None
+        return K_full, V_full, pos
 
     def get_memory_stats(self) -> dict:
         """spectral_cache.py:614-655 with the bytes this cache actually stores."""
