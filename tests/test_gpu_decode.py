@@ -205,6 +205,25 @@ def test_block_split_variants(with_logits):
         _run(states, Q, cos, sin, total - 1, "absolute", split=3, with_logits=with_logits)
 
 
+def test_records_merged_over_several_chunks():
+    """72 partial records per query head (9 cold blocks split over 8
+    workgroups each): the combine merges them 32 at a time, the last chunk
+    partly filled.  Outputs meet the oracle's bar; split 1 (10 records, one
+    chunk) agrees within a few fp16 ulps."""
+    rng = np.random.default_rng(21)
+    states = [random_state(rng, 2, 128, 9, 512, 16, 32, 100)]
+    total = states[0].total_tokens()
+    cos, sin = rope_tables(total + 8, 128)
+    Q = rng.standard_normal((1, 8, 128)).astype(np.float16)
+    ref, _, _ = o_abs(Q[0], states[0], cos, sin, total - 1)
+    out8, _ = _run(states, Q, cos, sin, total - 1, "absolute", split=8, with_logits=False)
+    out1, _ = _run(states, Q, cos, sin, total - 1, "absolute", split=1, with_logits=False)
+    ref = ref.astype(np.float64)
+    assert np.abs(out8[0] - ref).max() <= ATOL
+    assert np.abs(out8[0] - ref).max() <= RTOL_MAX * np.abs(ref).max()
+    assert np.abs(out8[0] - out1[0]).max() <= 4 * _ulp16(np.abs(out1[0]).max())
+
+
 def test_rope_none_equals_dense_unrotated():
     from unsloth_spectral import _lib
     from unsloth_spectral._decode import run_decode

@@ -149,10 +149,14 @@ __global__ __launch_bounds__(kThreads) void prefill_kernel(PrefillParams p) {
         ls += e;
       }
       l = l * alpha + sum_over_rows(ls);
+      // alpha is exactly 1 where the maximum did not grow: the accumulators
+      // are rescaled only when some query of the wave saw a larger score
+      if (__any(mn > m)) {
 #pragma unroll
-      for (int i = 0; i < 8; ++i) od[i] *= alpha;
+        for (int i = 0; i < 8; ++i) od[i] *= alpha;
 #pragma unroll
-      for (int i = 0; i < NTV; ++i) ok[i] *= alpha;
+        for (int i = 0; i < NTV; ++i) ok[i] *= alpha;
+      }
       m = mn;
     }
     return pp;
