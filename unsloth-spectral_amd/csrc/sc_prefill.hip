@@ -6,8 +6,10 @@
 // their absolute positions with apply_rope, spectral_attention.py:80-114,
 // which uses the first half of the cos/sin rows for both halves).
 //
-// Workgroup = (sequence b, KV head h, 16 query tokens); its four waves are
-// the four query heads of h (GQA group of 4).  Per 16-token key tile:
+// Workgroup = (sequence b, KV head h, 32 query tokens); its four waves are
+// the four query heads of h (GQA group of 4), each over two 16-query
+// sub-tiles, so every reconstructed key tile serves 128 (query, head)
+// pairs.  Per 16-token key tile:
 //   * cold block: the waves reconstruct K^T = B_K . C^T on MFMA from the
 //     INT8 codes (coefficients fp16(code * scale), as the reference stores
 //     them), two 16-row d tiles each (d and d + 64, so every RoPE pair is
@@ -28,7 +30,8 @@
 namespace {
 
 constexpr int kThreads = 256;
-constexpr int kQT = 16;            // query tokens per workgroup
+constexpr int kQS = 2;             // 16-query sub-tiles per wave
+constexpr int kQT = 16 * kQS;      // query tokens per workgroup
 constexpr int kKT = 16;            // key tokens per tile
 constexpr int kPitch = 128 + 8;    // LDS row pitch (halves) of a K or V tile
 constexpr int kTile = kKT * kPitch;  // halves per LDS tile
@@ -79,7 +82,7 @@ __device__ __forceinline__ void rope_rows(const PrefillParams& p, int pos, int d
 }
 
 template <int KK, int KV>
-__global__ __launch_bounds__(kThreads) void prefill_kernel(PrefillParams p) {
+__global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(2))) void prefill_kernel(PrefillParams p) {
   __shared__ __align__(16) h16 kbuf[2][kTile];
   __shared__ __align__(16) h16 vbuf[2][kTile];
   const ScTierDesc& t = p.t;
@@ -90,76 +93,93 @@ __global__ __launch_bounds__(kThreads) void prefill_kernel(PrefillParams p) {
   const int b = bh / t.kv_heads, h = bh % t.kv_heads;
   const int qh = h * 4 + w;
   const int q0 = qt * kQT;
-  const int qi = q0 + n;  // this lane's query column
-  const bool qvalid = qi < p.Tq;
-  const int qpos = qvalid ? p.qpos[b * p.qpos_sb + qi] : -1;
+  int qi[kQS], qpos[kQS];  // this lane's query column in each sub-tile
+  bool qvalid[kQS];
   // largest query position of the workgroup (keys beyond it are skipped)
-  int qmax = qpos;
+  int qmax = -1;
+#pragma unroll
+  for (int u = 0; u < kQS; ++u) {
+    qi[u] = q0 + 16 * u + n;
+    qvalid[u] = qi[u] < p.Tq;
+    qpos[u] = qvalid[u] ? p.qpos[b * p.qpos_sb + qi[u]] : -1;
+    qmax = max(qmax, qpos[u]);
+  }
 #pragma unroll
   for (int o = 1; o < 16; o <<= 1) qmax = max(qmax, __shfl_xor(qmax, o));
-  // Q^T operand: lane (g, n) supplies Q[q n][32 s + 8 g .. +7]
-  half8_t qb[4];
-  {
-    const h16* qr = p.q + b * p.q_sb + (long)qh * p.q_sh + (long)(qvalid ? qi : 0) * p.q_st;
+  // Q^T operands: lane (g, n) supplies Q[q n of sub-tile u][32 s + 8 g .. +7]
+  half8_t qb[kQS][4];
+#pragma unroll
+  for (int u = 0; u < kQS; ++u) {
+    const h16* qr = p.q + b * p.q_sb + (long)qh * p.q_sh + (long)(qvalid[u] ? qi[u] : 0) * p.q_st;
 #pragma unroll
     for (int s = 0; s < 4; ++s)
-      qb[s] = qvalid ? *reinterpret_cast<const half8_t*>(qr + 32 * s + 8 * g) : (half8_t)(h16)0;
+      qb[u][s] = qvalid[u] ? *reinterpret_cast<const half8_t*>(qr + 32 * s + 8 * g) : (half8_t)(h16)0;
   }
   constexpr int NTV = KV / 16;
-  float m = -INFINITY, l = 0.f;
-  float4_t od[8], ok[NTV];
+  float m[kQS], l[kQS];
+  float4_t od[kQS][8], ok[kQS][NTV];
 #pragma unroll
-  for (int i = 0; i < 8; ++i) od[i] = (float4_t)0.f;
+  for (int u = 0; u < kQS; ++u) {
+    m[u] = -INFINITY;
+    l[u] = 0.f;
 #pragma unroll
-  for (int i = 0; i < NTV; ++i) ok[i] = (float4_t)0.f;
+    for (int i = 0; i < 8; ++i) od[u][i] = (float4_t)0.f;
+#pragma unroll
+    for (int i = 0; i < NTV; ++i) ok[u][i] = (float4_t)0.f;
+  }
   const int32_t* cnt = t.counters + b * SC_NCOUNTERS;
   const int ncold = cnt[SC_CNT_NCOLD];
   const bool per_row = t.granularity == SC_QUANT_PER_ROW;
   int buf = 0;
 
-  // Scores of the tile in kbuf[buf], masked, folded into the softmax state;
-  // returns P^T (lane (g, n): P[tok 4g + j][q n]) as fp16.
-  auto scores = [&](const int (&kpos)[4]) __attribute__((always_inline)) -> half4_t {
-    float4_t sacc = (float4_t)0.f;
+  // Scores of the tile in kbuf[buf] against each query sub-tile, masked,
+  // folded into the sub-tile's softmax state; pp[u] = P^T (lane (g, n):
+  // P[tok 4g + j][q n of sub-tile u]) as fp16.
+  auto scores = [&](const int (&kpos)[4], half4_t (&pp)[kQS]) __attribute__((always_inline)) {
     const h16* kr = kbuf[buf] + n * kPitch;
+    half8_t ka[4];
 #pragma unroll
-    for (int s = 0; s < 4; ++s)
-      sacc = mfma_16x16x32(*reinterpret_cast<const half8_t*>(kr + 32 * s + 8 * g), qb[s], sacc);
-    float sv[4];
-    float tmax = -INFINITY;
+    for (int s = 0; s < 4; ++s) ka[s] = *reinterpret_cast<const half8_t*>(kr + 32 * s + 8 * g);
 #pragma unroll
-    for (int j = 0; j < 4; ++j) {
-      // reference rounding: fp16 matmul output, then fp16 after the scaling
-      const float s16 = (float)(h16)sacc[j];
-      float v = (float)(h16)(s16 * p.scale);
-      if (!qvalid || kpos[j] < 0 || kpos[j] > qpos) v = -INFINITY;
-      sv[j] = v;
-      tmax = fmaxf(tmax, v);
-    }
-    tmax = max_over_rows(tmax);
-    const float mn = fmaxf(m, tmax);
-    half4_t pp = (half4_t)(h16)0;
-    if (mn != -INFINITY) {
-      const float alpha = __expf(m - mn);  // m = -inf: 0
-      float ls = 0.f;
+    for (int u = 0; u < kQS; ++u) {
+      float4_t sacc = (float4_t)0.f;
+#pragma unroll
+      for (int s = 0; s < 4; ++s) sacc = mfma_16x16x32(ka[s], qb[u][s], sacc);
+      float sv[4];
+      float tmax = -INFINITY;
 #pragma unroll
       for (int j = 0; j < 4; ++j) {
-        const float e = sv[j] == -INFINITY ? 0.f : __expf(sv[j] - mn);
-        pp[j] = (h16)e;
-        ls += e;
+        // reference rounding: fp16 matmul output, then fp16 after the scaling
+        const float s16 = (float)(h16)sacc[j];
+        float v = (float)(h16)(s16 * p.scale);
+        if (!qvalid[u] || kpos[j] < 0 || kpos[j] > qpos[u]) v = -INFINITY;
+        sv[j] = v;
+        tmax = fmaxf(tmax, v);
       }
-      l = l * alpha + sum_over_rows(ls);
-      // alpha is exactly 1 where the maximum did not grow: the accumulators
-      // are rescaled only when some query of the wave saw a larger score
-      if (__any(mn > m)) {
+      tmax = max_over_rows(tmax);
+      const float mn = fmaxf(m[u], tmax);
+      pp[u] = (half4_t)(h16)0;
+      if (mn != -INFINITY) {
+        const float alpha = __expf(m[u] - mn);  // m = -inf: 0
+        float ls = 0.f;
 #pragma unroll
-        for (int i = 0; i < 8; ++i) od[i] *= alpha;
+        for (int j = 0; j < 4; ++j) {
+          const float e = sv[j] == -INFINITY ? 0.f : __expf(sv[j] - mn);
+          pp[u][j] = (h16)e;
+          ls += e;
+        }
+        l[u] = l[u] * alpha + sum_over_rows(ls);
+        // alpha is exactly 1 where the maximum did not grow: the accumulators
+        // are rescaled only when some query of the wave saw a larger score
+        if (__any(mn > m[u])) {
 #pragma unroll
-        for (int i = 0; i < NTV; ++i) ok[i] *= alpha;
+          for (int i = 0; i < 8; ++i) od[u][i] *= alpha;
+#pragma unroll
+          for (int i = 0; i < NTV; ++i) ok[u][i] *= alpha;
+        }
+        m[u] = mn;
       }
-      m = mn;
     }
-    return pp;
   };
 
   // ---------------------------------------------------------------- cold blocks
@@ -253,38 +273,47 @@ __global__ __launch_bounds__(kThreads) void prefill_kernel(PrefillParams p) {
       int kpos[4];
 #pragma unroll
       for (int e = 0; e < 4; ++e) kpos[e] = start + tok0 + 4 * g + e;
-      const half4_t pp = scores(kpos);
+      half4_t pp[kQS];
+      scores(kpos, pp);
       // ---- values in rank space: O_k^T[16 nt + n][q] += C_V[tok 4g + e][16 nt + n] * P[tok][q]
 #pragma unroll
       for (int nt = 0; nt < NTV; ++nt) {
         half4_t a;
 #pragma unroll
         for (int e = 0; e < 4; ++e) a[e] = (h16)((float)(int8_t)(cur.cv[nt] >> (8 * e)) * cur.sv4[e]);
-        ok[nt] = mfma_16x16x16(a, pp, ok[nt]);
+#pragma unroll
+        for (int u = 0; u < kQS; ++u) ok[u][nt] = mfma_16x16x16(a, pp[u], ok[u][nt]);
       }
       buf ^= 1;
       cur = nxt;
     }
     // ---- projection of the block: O_d^T[d][q] += B_V[d][k] O_k^T[k][q] (hi + lo fp16 parts)
-    half4_t ph[NTV], pl[NTV];
+    half4_t ph[kQS][NTV], pl[kQS][NTV];
 #pragma unroll
-    for (int nt = 0; nt < NTV; ++nt)
+    for (int u = 0; u < kQS; ++u)
 #pragma unroll
-      for (int e = 0; e < 4; ++e) {
-        const h16 hi = (h16)ok[nt][e];
-        ph[nt][e] = hi;
-        pl[nt][e] = (h16)(ok[nt][e] - (float)hi);
-      }
+      for (int nt = 0; nt < NTV; ++nt)
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+          const h16 hi = (h16)ok[u][nt][e];
+          ph[u][nt][e] = hi;
+          pl[u][nt][e] = (h16)(ok[u][nt][e] - (float)hi);
+        }
 #pragma unroll
     for (int mt = 0; mt < 8; ++mt)
 #pragma unroll
       for (int nt = 0; nt < NTV; ++nt) {
         const half4_t a = *reinterpret_cast<const half4_t*>(bv + (long)(16 * mt + n) * KV + 16 * nt + 4 * g);
-        od[mt] = mfma_16x16x16(a, ph[nt], od[mt]);
-        od[mt] = mfma_16x16x16(a, pl[nt], od[mt]);
+#pragma unroll
+        for (int u = 0; u < kQS; ++u) {
+          od[u][mt] = mfma_16x16x16(a, ph[u][nt], od[u][mt]);
+          od[u][mt] = mfma_16x16x16(a, pl[u][nt], od[u][mt]);
+        }
       }
 #pragma unroll
-    for (int i = 0; i < NTV; ++i) ok[i] = (float4_t)0.f;
+    for (int u = 0; u < kQS; ++u)
+#pragma unroll
+      for (int i = 0; i < NTV; ++i) ok[u][i] = (float4_t)0.f;
   }
 
   // ---------------------------------------------------------------- FP16 tail
@@ -327,29 +356,34 @@ __global__ __launch_bounds__(kThreads) void prefill_kernel(PrefillParams p) {
     *reinterpret_cast<half4_t*>(vbuf[buf] + n * kPitch + td1) = tcur.v1;
     *reinterpret_cast<half4_t*>(vbuf[buf] + n * kPitch + td1 + 64) = tcur.v2;
     __syncthreads();
-    const half4_t pp = scores(tcur.kpos);
+    half4_t pp[kQS];
+    scores(tcur.kpos, pp);
     // O_d^T[16 mt + n][q] += V[tok 4g + e][16 mt + n] P[tok][q]; V^T by transposing reads:
     // lane L of group g addresses row 4g + (L >> 2), columns 16 mt + 4 (L & 3)
 #pragma unroll
     for (int mt = 0; mt < 8; ++mt) {
       const h16* src = vbuf[buf] + (4 * g + (n >> 2)) * kPitch + 16 * mt + 4 * (n & 3);
       const short4_t r = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_s4*)src);
-      od[mt] = mfma_16x16x16(__builtin_bit_cast(half4_t, r), pp, od[mt]);
+#pragma unroll
+      for (int u = 0; u < kQS; ++u) od[u][mt] = mfma_16x16x16(__builtin_bit_cast(half4_t, r), pp[u], od[u][mt]);
     }
     buf ^= 1;
     tcur = tnxt;
   }
 
   // ---------------------------------------------------------------- output
-  if (qvalid) {
-    const float il = l > 0.f ? 1.f / l : 0.f;
-    h16* o = p.out + b * p.o_sb + (long)qh * p.o_sh + (long)qi * p.o_st;
 #pragma unroll
-    for (int mt = 0; mt < 8; ++mt) {
-      half4_t v;
+  for (int u = 0; u < kQS; ++u) {
+    if (qvalid[u]) {
+      const float il = l[u] > 0.f ? 1.f / l[u] : 0.f;
+      h16* o = p.out + b * p.o_sb + (long)qh * p.o_sh + (long)qi[u] * p.o_st;
 #pragma unroll
-      for (int e = 0; e < 4; ++e) v[e] = (h16)(od[mt][e] * il);
-      *reinterpret_cast<half4_t*>(o + 16 * mt + 4 * g) = v;
+      for (int mt = 0; mt < 8; ++mt) {
+        half4_t v;
+#pragma unroll
+        for (int e = 0; e < 4; ++e) v[e] = (h16)(od[u][mt][e] * il);
+        *reinterpret_cast<half4_t*>(o + 16 * mt + 4 * g) = v;
+      }
     }
   }
 }
