@@ -209,7 +209,7 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(2))) v
     }
     // tiles that hold a key at or before the last query of the workgroup
     const int ntl = min(t.block_size / kKT, (qmax - start) / kKT + 1);
-    // Global inputs of one tile, loaded a tile ahead of their use.
+    // Global inputs of one tile (loaded ahead of their use, see below).
     struct TileIn {
       uint2 ck[KC];   // K codes of token tok0 + n (KK = 16: 4 bytes in .x)
       float scl;      // its K scale
@@ -233,19 +233,15 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(2))) v
         in.cv[nt] = *reinterpret_cast<const uint32_t*>(cv + (long)(16 * nt + n) * t.block_size + tok0 + 4 * g);
       in.sv4 = per_row ? *reinterpret_cast<const float4_t*>(svp + tok0 + 4 * g) : (float4_t)svp[0];
     };
-    TileIn cur, nxt;
-    load_in(0, cur);
-    for (int tt = 0; tt < ntl; ++tt) {
-      const int tok0 = tt * kKT;
-      if (tt + 1 < ntl) load_in(tok0 + kKT, nxt);
-      // ---- reconstruct this wave's d tiles of K^T for tokens tok0 .. tok0 + 15
+    // Reconstruct + rotate the tile whose inputs are in `in` into kbuf[slot].
+    auto recon = [&](const TileIn& in, int slot) __attribute__((always_inline)) {
       float4_t x[2];
 #pragma unroll
       for (int u = 0; u < 2; ++u) x[u] = (float4_t)0.f;
       if constexpr (KK == 16) {
         half4_t cf;
 #pragma unroll
-        for (int e = 0; e < 4; ++e) cf[e] = (h16)((float)(int8_t)(cur.ck[0].x >> (8 * e)) * cur.scl);
+        for (int e = 0; e < 4; ++e) cf[e] = (h16)((float)(int8_t)(in.ck[0].x >> (8 * e)) * in.scl);
 #pragma unroll
         for (int u = 0; u < 2; ++u) x[u] = mfma_16x16x16(ak4[u], cf, x[u]);
       } else {
@@ -254,8 +250,8 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(2))) v
           half8_t cf;
 #pragma unroll
           for (int e = 0; e < 4; ++e) {
-            cf[e] = (h16)((float)(int8_t)(cur.ck[c].x >> (8 * e)) * cur.scl);
-            cf[4 + e] = (h16)((float)(int8_t)(cur.ck[c].y >> (8 * e)) * cur.scl);
+            cf[e] = (h16)((float)(int8_t)(in.ck[c].x >> (8 * e)) * in.scl);
+            cf[4 + e] = (h16)((float)(int8_t)(in.ck[c].y >> (8 * e)) * in.scl);
           }
 #pragma unroll
           for (int u = 0; u < 2; ++u) x[u] = mfma_16x16x32(ak[u][c], cf, x[u]);
@@ -268,8 +264,21 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(2))) v
         x1[e] = (h16)x[0][e];
         x2[e] = (h16)x[1][e];
       }
-      rope_rotate_store(x1, x2, cur.c, cur.s, d1, kbuf[buf] + n * kPitch);
-      __syncthreads();
+      rope_rotate_store(x1, x2, in.c, in.s, d1, kbuf[slot] + n * kPitch);
+    };
+    // Software pipeline over the tiles: tile tt + 1 is reconstructed into
+    // the other LDS buffer before tile tt's scores and values (independent
+    // work the scheduler can interleave), with one barrier per tile; the
+    // global inputs run two tiles ahead of their reconstruction.
+    TileIn cur, nxt, nx2;
+    load_in(0, cur);
+    if (ntl > 1) load_in(kKT, nxt);
+    recon(cur, buf);
+    __syncthreads();
+    for (int tt = 0; tt < ntl; ++tt) {
+      const int tok0 = tt * kKT;
+      if (tt + 2 < ntl) load_in(tok0 + 2 * kKT, nx2);
+      if (tt + 1 < ntl) recon(nxt, buf ^ 1);
       int kpos[4];
 #pragma unroll
       for (int e = 0; e < 4; ++e) kpos[e] = start + tok0 + 4 * g + e;
@@ -284,8 +293,10 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(2))) v
 #pragma unroll
         for (int u = 0; u < kQS; ++u) ok[u][nt] = mfma_16x16x16(a, pp[u], ok[u][nt]);
       }
+      __syncthreads();  // tile tt read by every wave; tile tt + 1 written
       buf ^= 1;
       cur = nxt;
+      nxt = nx2;
     }
     // ---- projection of the block: O_d^T[d][q] += B_V[d][k] O_k^T[k][q] (hi + lo fp16 parts)
     half4_t ph[kQS][NTV], pl[kQS][NTV];
