@@ -88,8 +88,12 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(2))) v
   const ScTierDesc& t = p.t;
   const int lane = threadIdx.x & 63, g = lane >> 4, n = lane & 15;
   const int w = threadIdx.x >> 6;
-  const int qt = blockIdx.x % p.nqt;
-  const int bh = blockIdx.x / p.nqt;
+  // Causal work grows with the query tile: workgroups are dispatched
+  // heaviest first (last query tile of every (sequence, head) first), so
+  // the light ones fill in at the end instead of a heavy one trailing.
+  const int nbh = p.t.batch * p.t.kv_heads;
+  const int qt = p.nqt - 1 - (int)(blockIdx.x / nbh);
+  const int bh = blockIdx.x % nbh;
   const int b = bh / t.kv_heads, h = bh % t.kv_heads;
   const int qh = h * 4 + w;
   const int q0 = qt * kQT;
