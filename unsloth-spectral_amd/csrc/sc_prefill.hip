@@ -110,6 +110,15 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(2))) v
   }
 #pragma unroll
   for (int o = 1; o < 16; o <<= 1) qmax = max(qmax, __shfl_xor(qmax, o));
+  // smallest query position of each sub-tile (-1 if a query is past t_q):
+  // key tiles entirely at or before it need no mask
+  int qmin[kQS];
+#pragma unroll
+  for (int u = 0; u < kQS; ++u) {
+    qmin[u] = qpos[u];
+#pragma unroll
+    for (int o = 1; o < 16; o <<= 1) qmin[u] = min(qmin[u], __shfl_xor(qmin[u], o));
+  }
   // Q^T operands: lane (g, n) supplies Q[q n of sub-tile u][32 s + 8 g .. +7]
   half8_t qb[kQS][4];
 #pragma unroll
@@ -139,7 +148,8 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(2))) v
   // Scores of the tile in kbuf[buf] against each query sub-tile, masked,
   // folded into the sub-tile's softmax state; pp[u] = P^T (lane (g, n):
   // P[tok 4g + j][q n of sub-tile u]) as fp16.
-  auto scores = [&](const int (&kpos)[4], half4_t (&pp)[kQS]) __attribute__((always_inline)) {
+  // kmax: largest key position of the tile (INT_MAX when unknown: always masked).
+  auto scores = [&](const int (&kpos)[4], int kmax, half4_t (&pp)[kQS]) __attribute__((always_inline)) {
     const h16* kr = kbuf[buf] + n * kPitch;
     half8_t ka[4];
 #pragma unroll
@@ -151,12 +161,13 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(2))) v
       for (int s = 0; s < 4; ++s) sacc = mfma_16x16x32(ka[s], qb[u][s], sacc);
       float sv[4];
       float tmax = -INFINITY;
+      const bool visible = kmax <= qmin[u];  // wave-uniform: every key before every query
 #pragma unroll
       for (int j = 0; j < 4; ++j) {
         // reference rounding: fp16 matmul output, then fp16 after the scaling
         const float s16 = (float)(h16)sacc[j];
         float v = (float)(h16)(s16 * p.scale);
-        if (!qvalid[u] || kpos[j] < 0 || kpos[j] > qpos[u]) v = -INFINITY;
+        if (!visible && (!qvalid[u] || kpos[j] < 0 || kpos[j] > qpos[u])) v = -INFINITY;
         sv[j] = v;
         tmax = fmaxf(tmax, v);
       }
@@ -287,7 +298,7 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(2))) v
 #pragma unroll
       for (int e = 0; e < 4; ++e) kpos[e] = start + tok0 + 4 * g + e;
       half4_t pp[kQS];
-      scores(kpos, pp);
+      scores(kpos, start + tok0 + kKT - 1, pp);
       // ---- values in rank space: O_k^T[16 nt + n][q] += C_V[tok 4g + e][16 nt + n] * P[tok][q]
 #pragma unroll
       for (int nt = 0; nt < NTV; ++nt) {
@@ -372,7 +383,7 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(2))) v
     *reinterpret_cast<half4_t*>(vbuf[buf] + n * kPitch + td1 + 64) = tcur.v2;
     __syncthreads();
     half4_t pp[kQS];
-    scores(tcur.kpos, pp);
+    scores(tcur.kpos, 0x7fffffff, pp);
     // O_d^T[16 mt + n][q] += V[tok 4g + e][16 mt + n] P[tok][q]; V^T by transposing reads:
     // lane L of group g addresses row 4g + (L >> 2), columns 16 mt + 4 (L & 3)
 #pragma unroll
