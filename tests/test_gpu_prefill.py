@@ -74,6 +74,26 @@ def test_prefill_matches_closed_form(case):
         _check(out[b], _closed_form(Q[b], states[b], cos, sin, qpos[b]))
 
 
+def test_prefill_shuffled_query_positions():
+    """Query tokens whose positions are not increasing (each sees the keys at
+    or before its own position): masks are decided per query, and the
+    fully-visible shortcut only for key tiles before every query of a
+    sub-tile."""
+    from unsloth_spectral._prefill import run_prefill
+    rng = np.random.default_rng(31)
+    states = [random_state(rng, 2, 128, 3, 128, 16, 32, 60, per_row=True)]
+    total = states[0].total_tokens()
+    cos, sin = rope_tables(total + 8, 128)
+    cache = cache_from_states(states, block_size=128)
+    Tq = 70
+    Q = rng.standard_normal((1, 8, Tq, 128)).astype(np.float16)
+    qpos = rng.permutation(np.asarray(states[0].positions()))[:Tq][None].astype(np.int32)
+    ct, sn = tables(cos, sin)
+    out = run_prefill(torch.from_numpy(Q).cuda(), cache, ct, sn, torch.from_numpy(qpos).cuda())
+    torch.cuda.synchronize()
+    _check(out[0].float().cpu().numpy(), _closed_form(Q[0], states[0], cos, sin, qpos[0]))
+
+
 def test_prefill_matches_dense_reference_path():
     """Against integration._dense_prefill (dense fp16 attention over get_kv,
     the reference's own prefill arithmetic) on the GPU."""
