@@ -1119,10 +1119,25 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(2))) v
 // one single-wave workgroup per query head, lane l owns d = E l .. E l + E - 1.
 // Records are merged U at a time with every load of a chunk in flight at
 // once: lane k (and k + U) loads the (m, l) header of record k, the chunk
-// maximum and the weighted sum of l are lane reductions, and the weight of
+// maximum and the weighted sum of l are register reductions, and the weight of
 // record k reaches every lane by readlane (an SGPR operand of the FMAs).
 // Every unit writes its record (m = -inf, l = 0, o = 0 when it saw no
 // token), so a weight of zero needs no branch.
+// Reduction over each 32-lane half of a wavefront in registers: DPP quad
+// permutes (lane ^ 1, lane ^ 2), row half-mirror and row mirror (every
+// 16-lane row), then v_permlane16_swap between the two rows of the half.
+template <bool MAX>
+__device__ __forceinline__ float half_reduce(float v) {
+  auto op = [](float a, float b) { return MAX ? fmaxf(a, b) : a + b; };
+  v = op(v, __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), 0xB1, 0xF, 0xF, false)));
+  v = op(v, __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), 0x4E, 0xF, 0xF, false)));
+  v = op(v, __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), 0x141, 0xF, 0xF, false)));
+  v = op(v, __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), 0x140, 0xF, 0xF, false)));
+  const uint32_t u = __float_as_uint(v);
+  auto b = __builtin_amdgcn_permlane16_swap(u, u, false, false);
+  return op(__uint_as_float(b[0]), __uint_as_float(b[1]));
+}
+
 template <int D>
 __global__ __launch_bounds__(64) void decode_combine_kernel(DecodeParams p) {
   constexpr int PREC = Geo<D>::PREC;
@@ -1160,15 +1175,12 @@ __global__ __launch_bounds__(64) void decode_combine_kernel(DecodeParams p) {
     // scheduler sinks them to their uses and the chunk costs two round trips.
     __builtin_amdgcn_sched_barrier(0);
     const float mk = has ? ml.x : -INFINITY;
-    float mc = mk;
-#pragma unroll
-    for (int o = U / 2; o > 0; o >>= 1) mc = fmaxf(mc, __shfl_xor(mc, o));
+    static_assert(U == 32, "one header per lane of each 32-lane half");
+    const float mc = half_reduce<true>(mk);
     const float mn = fmaxf(M, mc);
     if (mn == -INFINITY) continue;  // wave-uniform: nothing seen yet
     const float ck = mk == -INFINITY ? 0.f : fast_exp2(mk - mn);
-    float lc = has ? ml.y * ck : 0.f;
-#pragma unroll
-    for (int o = U / 2; o > 0; o >>= 1) lc += __shfl_xor(lc, o);
+    const float lc = half_reduce<false>(has ? ml.y * ck : 0.f);
     const float a = fast_exp2(M - mn);  // exp2(-inf) = 0 on the first chunk
     L = L * a + lc;
 #pragma unroll
