@@ -1090,18 +1090,20 @@ __device__ void cold_unit(const DecodeParams& p, int b, int hq, int j, char* sme
 }
 
 // Workgroup x runs on XCD x % 8 (round-robin dispatch).  Each XCD gets a
-// contiguous, equal share of the units in (sequence, head group)-major
-// order, so all records of a head group are written on one XCD and merged
-// there by the combine kernel; the two workgroups of a CU hold the same
-// block of two head groups and read the same cos/sin rows.
+// contiguous, equal share of the units in chunk-major order, so
+// concurrently running units of one XCD read the same cos/sin rows from
+// its L2.  Within the share, slots s and s + half (the two workgroups a CU
+// holds) take consecutive units, i.e. the same block for two head groups.
 template <int D, int KK, int KV, int TPW, bool GEN>
 __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(2))) void decode_partial_kernel(DecodeParams p) {
   extern __shared__ __align__(16) char smem[];
   const long xcd = blockIdx.x & 7, slot = blockIdx.x >> 3;
   const long c_lo = xcd * p.n_cold_units / 8, c_hi = (xcd + 1) * p.n_cold_units / 8;
   if (slot >= c_hi - c_lo) return;
-  const long u = c_lo + slot;
-  const int bq = (int)(u / p.cold_units), j = (int)(u % p.cold_units);
+  const long n = c_hi - c_lo, half = (n + 1) / 2;
+  const long u = c_lo + (slot < half ? 2 * slot : 2 * (slot - half) + 1);
+  const int nbq = p.B * p.n_hq;
+  const int j = (int)(u / nbq), bq = (int)(u % nbq);
   if constexpr (GEN) {
     if (p.rope_mode != SC_ROPE_NONE && !p.halves_equal)
       cold_unit<D, KK, KV, TPW, GEN, false, 2>(p, bq / p.n_hq, bq % p.n_hq, j, smem);
@@ -1143,16 +1145,8 @@ __global__ __launch_bounds__(64) void decode_combine_kernel(DecodeParams p) {
   constexpr int PREC = Geo<D>::PREC;
   constexpr int E = D / 64;  // d values per lane
   constexpr int U = 32;      // records per chunk (lanes k and k + 32 hold header k)
-  // The partial kernel gives XCD x the units of (sequence, head group)
-  // slice [x nbq / 8, (x + 1) nbq / 8); the query heads of those groups are
-  // merged on the same XCD, where the records were written.
-  const int xcd = blockIdx.x & 7, slot = blockIdx.x >> 3;
-  const int nbq = p.B * p.n_hq, qpg = kWaves * p.nrep;  // query heads per head group
-  const int g_lo = xcd * nbq / 8, g_hi = (xcd + 1) * nbq / 8;
-  if (slot >= (g_hi - g_lo) * qpg) return;
-  const int bq = g_lo + slot / qpg;
-  const int b = bq / p.n_hq, qh = (bq % p.n_hq) * qpg + slot % qpg;
-  if (qh >= p.Hq) return;  // a partly filled last head group
+  const int wq = blockIdx.x;
+  const int b = wq / p.Hq, qh = wq % p.Hq;
   const int h = qh / p.nrep, hh = qh % p.nrep;
   const int lane = threadIdx.x & 63;
   const int W = p.units_per_bh;
@@ -1359,12 +1353,7 @@ int launch(DecodeParams& p, hipStream_t s) {
     int rc = sc_launch_status("decode_partial_kernel");
     if (rc) return rc;
   }
-  long cslots = 0;
-  for (int x = 0; x < 8; ++x) {
-    const long ng = (x + 1) * (long)p.B * p.n_hq / 8 - x * (long)p.B * p.n_hq / 8;
-    if (ng * kWaves * p.nrep > cslots) cslots = ng * kWaves * p.nrep;
-  }
-  hipLaunchKernelGGL((decode_combine_kernel<D>), dim3((unsigned)(8 * cslots)), dim3(64), 0, s, p);
+  hipLaunchKernelGGL((decode_combine_kernel<D>), dim3(p.B * p.Hq), dim3(64), 0, s, p);
   return sc_launch_status("decode_combine_kernel");
 }
 
