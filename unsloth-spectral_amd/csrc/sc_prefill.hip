@@ -61,13 +61,19 @@ typedef __attribute__((address_space(3))) short4_t lds_s4;
 // cos / sin at the key's position), then store them as K[tok][d] into the
 // LDS tile row.
 __device__ __forceinline__ void rope_rotate_store(half4_t x1, half4_t x2, half4_t c, half4_t s, int d1, h16* krow) {
+  // two packed fp16 pairs per operand: every product and sum rounded to fp16
+  typedef h16 half2_v __attribute__((ext_vector_type(2)));
   half4_t o1, o2;
 #pragma unroll
-  for (int e = 0; e < 4; ++e) {
-    const h16 a = x1[e] * c[e], b = x2[e] * s[e];
-    const h16 a2 = x2[e] * c[e], b2 = x1[e] * s[e];
-    o1[e] = a - b;
-    o2[e] = a2 + b2;
+  for (int e = 0; e < 4; e += 2) {
+    const half2_v X1 = {x1[e], x1[e + 1]}, X2 = {x2[e], x2[e + 1]};
+    const half2_v C = {c[e], c[e + 1]}, S = {s[e], s[e + 1]};
+    const half2_v a = X1 * C, b = X2 * S, a2 = X2 * C, b2 = X1 * S;
+    const half2_v r1 = a - b, r2 = a2 + b2;
+    o1[e] = r1.x;
+    o1[e + 1] = r1.y;
+    o2[e] = r2.x;
+    o2[e + 1] = r2.y;
   }
   *reinterpret_cast<half4_t*>(krow + d1) = o1;
   *reinterpret_cast<half4_t*>(krow + d1 + 64) = o2;
