@@ -31,6 +31,7 @@ namespace {
 
 constexpr int kThreads = 256;
 constexpr int kQS = 2;             // 16-query sub-tiles per wave
+constexpr float kLog2e = 1.4426950408889634f;
 constexpr int kQT = 16 * kQS;      // query tokens per workgroup
 constexpr int kKT = 16;            // key tokens per tile
 constexpr int kPitch = 128 + 8;    // LDS row pitch (halves) of a K or V tile
@@ -181,11 +182,14 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(2))) v
       const float mn = fmaxf(m[u], tmax);
       pp[u] = (half4_t)(h16)0;
       if (mn != -INFINITY) {
-        const float alpha = __expf(m[u] - mn);  // m = -inf: 0
+        // base 2: exp(x - mn) = exp2(x log2e - mn log2e); masked scores (-inf)
+        // and the first tile's m = -inf give exp2(-inf) = 0
+        const float mnl = mn * kLog2e;
+        const float alpha = __builtin_amdgcn_exp2f(__builtin_fmaf(m[u], kLog2e, -mnl));
         float ls = 0.f;
 #pragma unroll
         for (int j = 0; j < 4; ++j) {
-          const float e = sv[j] == -INFINITY ? 0.f : __expf(sv[j] - mn);
+          const float e = __builtin_amdgcn_exp2f(__builtin_fmaf(sv[j], kLog2e, -mnl));
           pp[u][j] = (h16)e;
           ls += e;
         }
