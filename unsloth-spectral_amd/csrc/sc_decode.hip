@@ -5,28 +5,31 @@
 //   spectral_attention_forward  spectral_attention.py:117-349          (distance RoPE)
 // with one split-K kernel plus a log-sum-exp combine.
 //
-// Work unit = (sequence b, KV head h, chunk); one 256-thread workgroup.  A
-// cold chunk is up to 512 tokens of one cold block; wave w owns 16*TPW
-// consecutive tokens of it.  A tail chunk is 128 FP16 tail tokens.
+// Work unit = (sequence b, group of four KV heads hq, unit j); one
+// 256-thread workgroup whose wave w owns KV head 4 hq + w and its GQA group
+// of query heads.  Unit j walks cold block j / split (or its share of the
+// block when a block is split over `split` workgroups) in ranges of 64
+// tokens, then folds in FP16 tail tiles j, j + W, ... (16 tokens each; W
+// units per (sequence, head group)).  Each wave writes one
+// partial record (running max, sum, unnormalised output) per query head;
+// decode_combine_kernel merges the records of a (sequence, query head).
 //
-// Cold path, per wave (two phases over the wave's tiles of 16 tokens):
-//   0. every HBM load of the wave is issued up front (INT8 codes of K and V,
-//      per-row scales, the K basis as MFMA operands, Q), so a workgroup
-//      keeps its whole share of the block in flight at once;
-//   A. per tile: X^T = B_K^T . code^T on MFMA (codes -> fp16 exactly in
-//      registers; basis rows permuted so that a lane holds the RoPE pairs
-//      (d, d + D/2) of one token), RoPE of the reconstructed key in packed
-//      fp16 with the caller's cos/sin rows (phi = p, or max(q - p, 0) in
-//      distance mode), scores of the GQA group S = Y . Q^T on MFMA, times
-//      the row scale, rounded at the reference's fp16 cast points;
-//   B. one maximum over all the wave's scores (no running rescale);
+// Per range and wave (phases of consecutive ranges overlap: phase C of
+// range r - 1 runs after phase A of range r):
+//   A. per 16-token tile: X^T = B_K^T . code^T on MFMA (codes -> fp16
+//      exactly in registers; basis rows permuted so that a lane holds the
+//      RoPE pairs (d, d + D/2) of one token), RoPE of the reconstructed key
+//      in packed fp16 with the cos/sin rows staged in LDS (phi = p, or
+//      max(q - p, 0) in distance mode), scores of the GQA group
+//      S = Y . Q^T on MFMA, times the row scale, rounded at the reference's
+//      fp16 cast points; the next range's codes are loaded meanwhile;
+//   B. the range maximum merged into the running maximum (base 2);
 //   C. per tile: P = exp2(logit - max), Pacc^T += C_V^T . (P * s_V) on MFMA.
-// Token order inside a 64-token group is permuted (lane group g of a score
+// Token order inside a 64-token range is permuted (lane group g of a score
 // tile holds tokens 16g + 4i + j of tile i) so that the V codes of four
 // tiles are one 16-byte load per lane and per-row scales are one coalesced
-// load per 64 tokens, broadcast with ds_swizzle.  The four waves merge in
-// LDS and the merged P.C_V of every query head is projected once through
-// B_V (d-major).
+// load per 64 tokens.  After the last range, Pacc is projected once through
+// B_V (d-major) and added to the tail tile's output.
 //
 // GEN = false is the branch-free path (RoPE absolute or distance over an
 // HF table whose halves are equal, no mask, no logits output); GEN = true
