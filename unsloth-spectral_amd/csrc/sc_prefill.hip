@@ -365,10 +365,17 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(2))) v
     int kpos[4];
   };
   const int td1 = 16 * w + 4 * g;
+  // Ring slot of tail token i < tl: head < capacity and tl <= capacity, so
+  // one conditional subtraction replaces the integer modulo; the clamp keeps
+  // even inconsistent counters inside the ring.
+  auto ring_slot = [&](int i) __attribute__((always_inline)) {
+    const int r = thead + i;
+    return min(r >= t.tail_capacity ? r - t.tail_capacity : r, t.tail_capacity - 1);
+  };
   auto load_tail = [&](int tok0, TailIn& in) __attribute__((always_inline)) {
     const int i = tok0 + n;
     const bool valid = i < tl;
-    const int slot = valid ? (thead + i) % t.tail_capacity : 0;
+    const int slot = valid ? ring_slot(i) : 0;
     const half4_t z = (half4_t)(h16)0;
     in.x1 = in.x2 = in.v1 = in.v2 = in.c = in.s = z;
     if (valid) {
@@ -381,7 +388,7 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(2))) v
 #pragma unroll
     for (int e = 0; e < 4; ++e) {
       const int ii = tok0 + 4 * g + e;
-      in.kpos[e] = ii < tl ? tp[(thead + ii) % t.tail_capacity] : -1;
+      in.kpos[e] = ii < tl ? tp[ring_slot(ii)] : -1;
     }
   };
   TailIn tcur, tnxt;
