@@ -161,3 +161,19 @@ def test_landmarks_come_first():
     assert pos.tolist() == [[0, 1, 2] + list(range(T + 40))]
     cache.reset()
     assert cache.landmark_K is None and cache.get_kv_with_landmarks() == (None, None, None)
+
+
+def test_landmarks_with_two_sequences():
+    """Positions are per sequence ([B, T]) for every tier."""
+    rng = np.random.default_rng(10)
+    H, D, T = 2, 128, 128
+    cache = _cache(H, D, T, weighted=False)
+    A = torch.from_numpy(rng.standard_normal((2, H, T + 8, D)).astype(np.float16)).cuda()
+    cache.append(A, A)
+    L = torch.from_numpy(rng.standard_normal((2, H, 1, D)).astype(np.float16)).cuda()
+    cache.add_landmarks(L, L, torch.tensor([[0], [0]], device="cuda"))
+    K, V, pos = cache.get_kv_with_landmarks()
+    assert K.shape == (2, H, 1 + T + 8, D) and pos.shape == (2, 1 + T + 8)
+    assert pos[:, 1:].tolist() == [list(range(T + 8))] * 2
+    Kc, _ = cache.get_kv()
+    assert torch.equal(K[:, :, 1:], Kc)

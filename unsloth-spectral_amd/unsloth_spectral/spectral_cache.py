@@ -473,8 +473,9 @@ class SpectralCache:
                                               _lib.stream_of(k)))
             K_parts.append(k)
             V_parts.append(v)
-            for s in self.block_start[0, :self._n_cold].tolist():
-                pos_parts.append(torch.arange(s, s + self.block_size, device=self.device).unsqueeze(0))
+            ar = torch.arange(self.block_size, device=self.device)
+            for j in range(self._n_cold):  # [B, T] positions of block j of every sequence
+                pos_parts.append(self.block_start[:, j:j + 1].to(torch.long) + ar)
         if self._B is not None and self.total_tokens > 0 and self._tail_len:
             K_parts.append(self.hot_K)
             V_parts.append(self.hot_V)
