@@ -106,19 +106,36 @@ def lowrank_kv(torch, seed, n, ctx, d, device, unit_scale=False):
     return out
 
 
+def orthonormal_columns(torch, X, passes=2):
+    """Orthonormal basis of the column space of each X [m, n, k] (n >= k):
+    CholeskyQR, twice.  The Gram matrices X^T X are formed in float64 on the
+    device; their k x k Cholesky factors and inverses are computed on the
+    host (LAPACK).  With positive Cholesky diagonals this is the Q factor of
+    QR with a positive R diagonal, so the distribution equals lowrank_kv's
+    (a Haar-distributed basis).  The device's own QR solver is not used."""
+    X = X.to(torch.float64)
+    for _ in range(passes):
+        G = torch.matmul(X.transpose(1, 2).contiguous(), X)
+        L = torch.linalg.cholesky(G.cpu())
+        Rinv = torch.linalg.inv(L.transpose(1, 2))
+        X = torch.matmul(X, Rinv.to(X.device))
+    return X
+
+
 def lowrank_kv_device(torch, seed, n, ctx, d, device, chunk=16):
     """Same distribution as lowrank_kv, drawn on the GPU (seeded device
-    generator, QR on the device) for the large batch-16 workload."""
+    generator, orthonormalised by orthonormal_columns) for the large batch-16
+    workload."""
     g = torch.Generator(device=device)
     g.manual_seed(seed)
-    sig = torch.exp(-torch.arange(d, dtype=torch.float32, device=device) / 8.0)
+    sig = torch.exp(-torch.arange(d, dtype=torch.float64, device=device) / 8.0)
     out = torch.empty(n, ctx, d, dtype=torch.float16, device=device)
     for i in range(0, n, chunk):
         m = min(chunk, n - i)
-        U, _ = torch.linalg.qr(torch.randn(m, ctx, d, generator=g, device=device))
-        V, _ = torch.linalg.qr(torch.randn(m, d, d, generator=g, device=device))
+        U = orthonormal_columns(torch, torch.randn(m, ctx, d, generator=g, device=device))
+        V = orthonormal_columns(torch, torch.randn(m, d, d, generator=g, device=device))
         out[i:i + m] = (torch.matmul(U * sig, V.transpose(1, 2).contiguous())
-                        + 0.01 * torch.randn(m, ctx, d, generator=g, device=device)).half()
+                        + 0.01 * torch.randn(m, ctx, d, generator=g, device=device, dtype=torch.float64)).half()
         del U, V
     return out
 
@@ -177,42 +194,77 @@ def decode_args(lib_mod, cache, Q, out, cos, sin, qpos, split=0):
     return a, tier
 
 
-def cpu_decode_baseline(cache, Q, cos, sin):
-    """The oracle (fp16-faithful restatement of spectral_attention_decode) on
-    every sequence of the same workload, timed on the host cores: the whole
-    batch-8 layer as 8 independent batch-1 caches (the reference's cache holds
-    one sequence), one call each."""
+def cpu_decode_baseline(cache, Q, cos, sin, mode="absolute", seqs=None):
+    """The oracle (fp16-faithful restatement of spectral_attention_decode,
+    absolute RoPE, or of spectral_attention_forward, distance RoPE) on the
+    same workload, timed on the host cores: each sequence as an independent
+    batch-1 cache (the reference's cache holds one sequence), one call each.
+    ``seqs`` bounds the sample to the first sequences of the batch (the rate
+    is per the sample's own bytes)."""
     import numpy as np
     from threadpoolctl import threadpool_info, threadpool_limits
     sys.path.insert(0, HERE)
-    from oracle.attention import ColdBlock, TierState, spectral_attention_decode
+    from oracle.attention import ColdBlock, TierState, spectral_attention_decode, spectral_attention_forward
+    fn = spectral_attention_decode if mode == "absolute" else spectral_attention_forward
     cores = len(os.sched_getaffinity(0))
-    nb = cache.num_cold_blocks
-    B = Q.shape[0]
+    nb, kK, kV = cache.num_cold_blocks, cache.k_rank_keys, cache.k_rank_values
+    B = Q.shape[0] if seqs is None else min(seqs, Q.shape[0])
+    ctx = nb * TB + cache.hot_len
     c, s = cos.cpu().numpy(), sin.cpu().numpy()
     hot_pos = cache.hot_position_ids.cpu().numpy()
     states = []
     for b in range(B):
-        ck = cache.codes_k[b, :, :nb, :, :K_RANK].cpu().numpy()
-        cv = cache.codes_v[b, :, :nb, :K_RANK, :].transpose(-1, -2).cpu().numpy()
+        ck = cache.codes_k[b, :, :nb, :, :kK].cpu().numpy()
+        cv = cache.codes_v[b, :, :nb, :kV, :].transpose(-1, -2).cpu().numpy()
         sk = cache.scales_k[b, :, :nb].cpu().numpy()
         sv = cache.scales_v[b, :, :nb].cpu().numpy()
-        bk = cache.basis_k[b, :, :nb, :, :K_RANK].transpose(-1, -2).cpu().numpy()
-        bv = cache.basis_v[b, :, :nb, :, :K_RANK].transpose(-1, -2).cpu().numpy()
+        bk = cache.basis_k[b, :, :nb, :, :kK].transpose(-1, -2).cpu().numpy()
+        bv = cache.basis_v[b, :, :nb, :, :kV].transpose(-1, -2).cpu().numpy()
         blocks = [ColdBlock(ck[:, j], sk[:, j], bk[:, j], cv[:, j], sv[:, j], bv[:, j], j * TB) for j in range(nb)]
         states.append(TierState(blocks, cache.hot_K[b].cpu().numpy(), cache.hot_V[b].cpu().numpy(), hot_pos[b]))
-    q = Q.cpu().numpy()
+    q = Q.reshape(Q.shape[0], HQ, D).cpu().numpy()
     with threadpool_limits(cores):
         blas = [i.get("num_threads") for i in threadpool_info()]
         t0 = time.perf_counter()
         for b in range(B):
-            spectral_attention_decode(q[b], states[b], c, s, CTX - 1)
+            fn(q[b], states[b], c, s, ctx - 1)
         sec = time.perf_counter() - t0
-    nbytes = decode_bytes(B, HKV, NBLK, K_RANK, K_RANK, TAIL)
+    nbytes = decode_bytes(B, HKV, nb, kK, kV, cache.hot_len, per_row=cache.quant_granularity == "per_row")
+    whole = "all" if B == Q.shape[0] else f"{B} of the {Q.shape[0]}"
     return {"value": round(nbytes / sec / 1e9, 4), "unit": "GB/s", "cores": max(b for b in blas if b) if blas else 1,
-            "kind": "port", "us_per_layer_batch8": round(sec * 1e6, 1),
-            "sample": f"oracle spectral_attention_decode (fp16-faithful numpy restatement), all {B} sequences of "
-                      f"the layer as independent batch-1 caches, absolute RoPE, one call each ({sec:.2f} s in all)"}
+            "kind": "port", "rope": mode, "us_per_sequence": round(sec / B * 1e6, 1),
+            "sample": f"oracle {fn.__name__} (fp16-faithful numpy restatement), {whole} sequences of one layer "
+                      f"(context {ctx}, {nb} cold blocks k={kK}/{kV}) as independent batch-1 caches, one call "
+                      f"each ({sec:.2f} s in all)"}
+
+
+def rsvd_rank32_parity(torch, M):
+    """Reconstruction error of the HIP rSVD at k=32 (r=37, the rank the
+    16K/33K workloads compress with) against the oracle's two restatements
+    with the same sketch: randomized_svd_ref (float32, no
+    re-orthonormalisation between power iterations, as rsvd.py:100-113) and
+    randomized_svd_subspace64 (the same subspace in float64).  Relative
+    differences (e_gpu - e_oracle) / e_oracle, per matrix."""
+    import numpy as np
+    sys.path.insert(0, HERE)
+    from oracle.rsvd import per_matrix_error, randomized_svd_ref, randomized_svd_subspace64
+    from unsloth_spectral import compress_matrices
+    g = torch.Generator().manual_seed(9)
+    omega = torch.randn(M.shape[0], D, 37, generator=g)
+    res = compress_matrices(M, 32, omega=omega.to(M.device), granularity="per_row", debug=True)
+    Mn = M.cpu().numpy()
+    e_gpu = per_matrix_error(Mn, res["coeffs"].cpu().numpy(), res["vh"].cpu().numpy())
+    out = {}
+    for name, fn in (("randomized_svd_ref", randomized_svd_ref), ("randomized_svd_subspace64", randomized_svd_subspace64)):
+        U, S, Vh = fn(Mn, 32, omega.numpy())
+        e = per_matrix_error(Mn, U * S[:, None, :], Vh)
+        rel = (e_gpu - e) / e
+        out[name] = {"recon_err": round(float(e.mean()), 6), "rel_diff_mean": round(float(rel.mean()), 6),
+                     "rel_diff_min": round(float(rel.min()), 6), "rel_diff_max": round(float(rel.max()), 6)}
+    out["gpu_recon_err"] = round(float(e_gpu.mean()), 6)
+    out["note"] = ("8 blocks 512x128 of the benchmark distribution, one fixed sketch; a negative difference "
+                   "means the HIP fit is closer than the oracle's")
+    return out
 
 
 def bench_rsvd(torch, hip, device, reps=20):
@@ -362,7 +414,7 @@ def compression_stall(torch, hip, cache_full, raw, reps=5):
 
 
 def decode_config(torch, lib, hip, device, b, nblk, k, tail, rotate, warmup, steps, on_device=False,
-                  stall=False):
+                  stall=False, cpu_seqs=0):
     """One secondary decode workload: event-timed call duration and the HBM
     roofline fraction of its algorithmic bytes."""
     log(f"building batch {b}, {nblk} cold blocks k={k}")
@@ -388,6 +440,10 @@ def decode_config(torch, lib, hip, device, b, nblk, k, tail, rotate, warmup, ste
                         "frac": round(ach / HBM_PEAK_GBS, 4)}}
     del caches
     log(f"batch {b}: {avg * 1e3:.2f} us per call")
+    if cpu_seqs:
+        log(f"CPU baselines (oracle), {cpu_seqs} sequence(s) of batch {b}, both RoPE modes")
+        res["cpu_baseline"] = {m: cpu_decode_baseline(cache0, Q, cos, sin, m, seqs=cpu_seqs)
+                               for m in ("absolute", "distance")}
     if stall:
         res["compression_stall"] = compression_stall(torch, hip, cache0, raw)
         log(f"compression stall: {res['compression_stall']}")
@@ -442,14 +498,16 @@ def model_loop(torch, device, prompt, decode_steps, layers=32):
             layer.self_attn._spectral_cache = None
         out, pre_s = timed(lambda: model(input_ids=ids[:, :n_prompt], use_cache=False, logits_to_keep=1))
         tok = out.logits[:, -1].argmax(-1)
+        pos_all = torch.arange(n_prompt, n_prompt + steps, device=device)[None]   # positions stay on the device
         torch.cuda.synchronize()
         t = time.perf_counter()
         for i in range(steps):
-            pos = torch.tensor([[n_prompt + i]], device=device)
-            out = model(input_ids=tok[:, None], position_ids=pos, use_cache=False, logits_to_keep=1)
+            out = model(input_ids=tok[:, None], position_ids=pos_all[:, i:i + 1], use_cache=False,
+                        logits_to_keep=1)
             tok = out.logits[:, -1].argmax(-1)
+        host_s = time.perf_counter() - t          # the host issued every step without waiting
         torch.cuda.synchronize()
-        return pre_s, time.perf_counter() - t
+        return pre_s, time.perf_counter() - t, host_s
 
     dense_run(min(prompt, 1024), 4)                      # warm-up (kernels, allocator)
     dense_s = dense_run(prompt, decode_steps)
@@ -457,7 +515,7 @@ def model_loop(torch, device, prompt, decode_steps, layers=32):
     torch.cuda.empty_cache()
     patch_unsloth_attention(model, k_rank_keys=16, k_rank_values=16, verbose=False, quant_granularity="per_row")
     spectral_run(min(prompt, 1024) + 8, 4)
-    prefill_s, spec_s = spectral_run(prompt, decode_steps)
+    prefill_s, spec_s, host_s = spectral_run(prompt, decode_steps)
     log(f"spectral cache: {spec_s / decode_steps * 1e3:.2f} ms per token, prefill {prefill_s:.2f} s")
     st = get_cache_stats(model)
     # decode attention of one token over every layer's final cache (HIP events)
@@ -496,6 +554,7 @@ def model_loop(torch, device, prompt, decode_steps, layers=32):
                                "(K and V), per-row INT8 scales, absolute RoPE theta 1e6",
                    "prompt": prompt, "decode_steps": decode_steps, "layers": layers},
         "spectral": {"decode_ms_per_token": round(spec_s / decode_steps * 1e3, 3),
+                     "host_issue_ms_per_token": round(host_s / decode_steps * 1e3, 3),
                      "prefill_s": round(prefill_s, 3),
                      "cold_blocks_per_layer": st["total_blocks"] // layers,
                      "compressions_during_decode": (prompt + decode_steps) // TB - prompt // TB,
@@ -668,7 +727,9 @@ def main():
     ap.add_argument("--only-headline", action="store_true",
                     help="time only the batch-8 decode workload and the rSVD (profiling runs)")
     ap.add_argument("--model-loop", action="store_true",
-                    help="run the Mistral-7B-shaped model loop instead and print its JSON line")
+                    help="run only the Mistral-7B-shaped model loop and print its JSON line")
+    ap.add_argument("--no-model-loop", action="store_true",
+                    help="leave the model loop out of the default line (profiling runs)")
     ap.add_argument("--split", type=int, default=0,
                     help="workgroups per cold block for the batch-8 workload (0 = library's choice)")
     ap.add_argument("--prompt", type=int, default=8192)
@@ -721,13 +782,16 @@ def main():
         "timing rSVD")
     M_rsvd, omega, rsvd = bench_rsvd(torch, hip, device)
     cpu = cpu_rsvd = None
+    cpu_dist = None
     if not args.no_cpu:
-        log("CPU baselines (oracle)")
+        log("CPU baselines (oracle), batch 8: absolute and distance RoPE")
         cpu = cpu_decode_baseline(cache0, Q.view(B, HQ, D), cos, sin)
+        cpu_dist = cpu_decode_baseline(cache0, Q.view(B, HQ, D), cos, sin, "distance")
         cpu_rsvd = cpu_rsvd_baseline(M_rsvd, omega)
         rsvd["cpu_baseline"] = cpu_rsvd
         rsvd["recon_err_rel_diff_vs_oracle"] = round(abs(rsvd["recon_err"] - cpu_rsvd["recon_err"])
                                                      / cpu_rsvd["recon_err"], 5)
+        rsvd["rank32_parity"] = rsvd_rank32_parity(torch, M_rsvd)
     others = None
     if not args.only_headline:
         log("block wire format: pack / unpack of the batch-8 tiers")
@@ -736,13 +800,18 @@ def main():
         torch.cuda.empty_cache()
         log("decode batch 1 (4K) and batch 16 (33K, with compression stall)")
         others = {
-            "batch1_ctx4096": decode_config(torch, lib, hip, device, 1, 7, 16, 512, args.rotate, 1000, 200),
+            "batch1_ctx4096": decode_config(torch, lib, hip, device, 1, 7, 16, 512, args.rotate, 1000, 200,
+                                            cpu_seqs=0 if args.no_cpu else 1),
             "batch16_ctx33280": decode_config(torch, lib, hip, device, 16, 64, 32, 512, 2, 300, 100,
-                                              on_device=True, stall=True),
+                                              on_device=True, stall=True, cpu_seqs=0 if args.no_cpu else 2),
             "block_wire_format": wire,
         }
         log("prefill attention, 8192-token prompt over 16 cold blocks")
         others["prefill_ctx8192"] = bench_prefill(torch, hip, device)
+        if not args.no_model_loop:
+            torch.cuda.empty_cache()
+            log("model loop: Mistral-7B shape, 8192-token prompt + 256 greedy steps")
+            others["model_loop"] = model_loop(torch, device, args.prompt, args.decode_steps)
     res = {
         "metric": "decode attn µs/layer + HBM GB/s (% peak) at 16K ctx; rSVD blocks/sec",
         "value": round(nb / (ms_per_step * 1e-3) / 1e9, 2),
@@ -771,6 +840,7 @@ def main():
                      "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": traffic,
                      "kernel": "sc_decode_attn call (decode_partial_kernel + decode_combine_kernel)"},
         "cpu_baseline": cpu,
+        "cpu_baseline_distance_rope": cpu_dist,
         "rsvd": rsvd,
         "other_decode_workloads": others,
     }

@@ -31,7 +31,7 @@
 extern "C" {
 #endif
 
-#define SC_ABI_VERSION 5
+#define SC_ABI_VERSION 6
 
 #define SC_OK 0
 #define SC_ERR_INVALID (-1)      /* bad argument / shape */
@@ -58,6 +58,9 @@ extern "C" {
 #define SC_CNT_NEXT_POS 3     /* reference current_position              */
 #define SC_CNT_TOTAL 4        /* reference total_tokens                  */
 #define SC_CNT_COMPRESSIONS 5 /* reference compression_count             */
+#define SC_CNT_STATUS 6       /* SC_ERR_CAPACITY after an append that did
+                                 not fit the ring (nothing was written);
+                                 0 otherwise; cleared by a reset          */
 #define SC_NCOUNTERS 8
 
 /*
@@ -159,6 +162,42 @@ int sc_decode_workspace_size(const ScDecodeArgs* args, size_t* bytes);
 int sc_decode_attn(const ScDecodeArgs* args, void* workspace, size_t workspace_bytes,
                    void* stream);
 
+
+/*
+ * Scores of one block against every query head, absolute RoPE
+ * (spectral_score_forward, kernels/spectral_attention.py:375-453):
+ *   scores[b][h][t] = fp16( sum_i (R^-1_{start+t} q[b][h]) . basis_k[g][i]
+ *                           * coeffs_k[g][t][i] ),  g = h / (q_heads/kv_heads)
+ * with the inverse rotation in fp16 elementwise arithmetic as the
+ * reference's _apply_inverse_rope (:340-372; halves of cos/sin as given)
+ * and the products summed in fp32.
+ *   q        fp16 [batch][q_heads][head_dim], element strides (16-byte rows)
+ *   coeffs_k fp16 [kv_heads][tokens][rank] (dequantised coefficients)
+ *   basis_k  fp16 [kv_heads][rank][head_dim] (16-byte aligned)
+ *   cos/sin  fp16 [rope_len][head_dim], row stride rope_stride; key
+ *            positions start_position .. start_position + tokens - 1 must
+ *            lie inside the tables
+ *   scores   fp16 [batch][q_heads][tokens]
+ * Supported: head_dim 64 or 128, rank <= 64.
+ */
+int sc_block_scores(const void* q, int64_t q_stride_b, int64_t q_stride_h, int32_t batch, int32_t q_heads,
+                    const void* coeffs_k, const void* basis_k, int32_t kv_heads, int32_t tokens, int32_t rank,
+                    int32_t head_dim, const void* cos, const void* sin, int64_t rope_stride, int32_t rope_len,
+                    int32_t start_position, void* scores, void* stream);
+
+/*
+ * Values of one block (spectral_value_forward,
+ * kernels/spectral_attention.py:544-601):
+ *   out[b][h] = fp16( (attn[b][h] . coeffs_v[g]) . basis_v[g] ), fp32 sums
+ *   attn     fp32 [batch][q_heads][tokens], element strides
+ *   coeffs_v fp16 [kv_heads][tokens][rank], basis_v fp16 [kv_heads][rank][head_dim]
+ *   out      fp16 [batch][q_heads][head_dim]
+ * Supported: head_dim 64 or 128, rank <= 64.
+ */
+int sc_block_values(const float* attn, int64_t attn_stride_b, int64_t attn_stride_h, int32_t batch,
+                    int32_t q_heads, const void* coeffs_v, const void* basis_v, int32_t kv_heads, int32_t tokens,
+                    int32_t rank, int32_t head_dim, void* out, void* stream);
+
 /*
  * Batched block compression: randomized SVD (rsvd.py:74-157, k = rank,
  * oversampling, n_iter) of `count` matrices [rows][cols] (fp16, fp32 or
@@ -237,13 +276,24 @@ int sc_quantize_int8(const float* x, int64_t groups, int64_t rows, int64_t cols,
  *   k_new, v_new fp16 [batch][kv_heads][t_new][head_dim] with element
  *   strides (stride_b, stride_h, stride_t; innermost contiguous);
  *   positions int32 [batch][t_new] (NULL = continue from NEXT_POS).
- * A first position below NEXT_POS resets the sequence's counters first
- * (new-generation detection, spectral_cache.py:176-189).
+ * flags:
+ *   SC_APPEND_RESET        every sequence starts a new generation: its
+ *                          counters are cleared before the rows are written
+ *                          (the caller detected the restart, as the
+ *                          reference does on the host, :176-189);
+ *   SC_APPEND_DETECT_RESET the device detects it per sequence: a first
+ *                          position below NEXT_POS resets that sequence.
  * Fails with SC_ERR_CAPACITY (before launching) if t_new exceeds the ring.
+ * On the device, a sequence whose tail would exceed tail_capacity gets
+ * nothing written, keeps its counters and has SC_CNT_STATUS set to
+ * SC_ERR_CAPACITY (the reference grows its tail with torch.cat and never
+ * overflows; here the caller sizes the ring or compresses first).
  */
+#define SC_APPEND_DETECT_RESET 1
+#define SC_APPEND_RESET 2
 int sc_tier_append(const ScTierDesc* tier, const void* k_new, const void* v_new,
                    int64_t stride_b, int64_t stride_h, int64_t stride_t,
-                   const int32_t* positions, int32_t t_new, void* stream);
+                   const int32_t* positions, int32_t t_new, int32_t flags, void* stream);
 
 /*
  * Compress every full block of every sequence's tail into the next cold

@@ -269,3 +269,39 @@ def closed_form64(Q, state, cos, sin, query_position, scale=None, mask=None, mod
     e = np.exp(logits - m)
     P = e / e.sum(axis=-1, keepdims=True)
     return np.einsum("ht,htd->hd", P, Vr), logits
+
+
+def spectral_score_forward(Q, coeffs_k, basis_k, cos, sin, start_position):
+    """Scores of one block, kernels/spectral_attention.py:375-453
+    (spectral_score_forward_pytorch): Q [Hq, D] fp16 post-RoPE, coeffs_k
+    fp16 [Hkv, T, k], basis_k fp16 [Hkv, k, D].  Q is inverse-rotated at each
+    key's absolute position with fp16 elementwise arithmetic (:411-425,
+    _apply_inverse_rope :340-372), projected on the repeated basis in fp32
+    (:436-440), multiplied by the coefficients and summed in fp32 (:444-445),
+    cast to fp16 (:446).  Returns fp16 [Hq, T]."""
+    Q = _h(Q)
+    Hq, D = Q.shape
+    Hkv, T, k = coeffs_k.shape
+    nrep = Hq // Hkv
+    kp = np.arange(int(start_position), int(start_position) + T)
+    cos, sin = _h(cos), _h(sin)
+    qa = _rope_halves(Q[:, None, :], cos[kp][None], (-sin[kp])[None])        # [Hq, T, D] fp16
+    basis = np.repeat(_h(basis_k), nrep, axis=0).astype(f32)                 # [Hq, k, D]
+    coeffs = np.repeat(_h(coeffs_k), nrep, axis=0).astype(f32)               # [Hq, T, k]
+    lat = np.matmul(qa.astype(f32), basis.transpose(0, 2, 1))               # [Hq, T, k]
+    return (lat * coeffs).sum(-1).astype(f16)
+
+
+def spectral_value_forward(attn, coeffs_v, basis_v):
+    """Values of one block, kernels/spectral_attention.py:544-601
+    (spectral_value_forward_pytorch): attn [Hq, T] in fp32 (:585), coeffs_v
+    fp16 [Hkv, T, k], basis_v fp16 [Hkv, k, D]; v_lat = attn . C in fp32
+    (:587), out = v_lat . B in fp32 (:593), cast to fp16 (:594).
+    Returns fp16 [Hq, D]."""
+    attn = np.asarray(attn, f32)
+    Hq = attn.shape[0]
+    nrep = Hq // coeffs_v.shape[0]
+    cv = np.repeat(_h(coeffs_v), nrep, axis=0).astype(f32)
+    bv = np.repeat(_h(basis_v), nrep, axis=0).astype(f32)
+    vl = np.einsum("ht,htk->hk", attn, cv)
+    return np.einsum("hk,hkd->hd", vl, bv).astype(f16)

@@ -20,9 +20,11 @@ def orthonormal_rows(rng, k, d):
 
 
 def random_state(rng, H, D, nblk, T, kK, kV, tail, per_row=False, start=0, coeff_std=1.5,
-                 tail_std=0.75, tail_pos=None):
+                 tail_std=0.75, tail_pos=None, batched_qr=False):
     """A tier state for one sequence: cold blocks with quantised Gaussian
-    coefficients and orthonormal fp16 bases, plus an fp16 tail."""
+    coefficients and orthonormal fp16 bases, plus an fp16 tail.
+    batched_qr draws the bases of all heads of a block with one stacked QR
+    (faster for large geometries; a different random stream)."""
     blocks = []
     for j in range(nblk):
         out = []
@@ -33,7 +35,11 @@ def random_state(rng, H, D, nblk, T, kK, kV, tail, per_row=False, start=0, coeff
                 codes, scale, _, _ = quantize_per_row(coeffs)
             else:
                 codes, scale, _, _ = quantize_per_head(coeffs)
-            basis = np.stack([orthonormal_rows(rng, k, D) for _ in range(H)]).astype(np.float16)
+            if batched_qr:
+                q, _ = np.linalg.qr(rng.standard_normal((H, D, k)))
+                basis = q.transpose(0, 2, 1).astype(np.float16)
+            else:
+                basis = np.stack([orthonormal_rows(rng, k, D) for _ in range(H)]).astype(np.float16)
             out.append((codes, scale, basis))
         (ck, sk, bk), (cv, sv, bv) = out
         blocks.append(ColdBlock(ck, sk, bk, cv, sv, bv, start + j * T))

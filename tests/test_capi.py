@@ -24,7 +24,8 @@ def test_header_declares_the_api():
     names = _declared_functions()
     for fn in ("sc_decode_attn", "sc_decode_workspace_size", "sc_rsvd_compress", "sc_quantize_int8",
                "sc_tier_append", "sc_tier_compress", "sc_tier_dequant", "sc_last_error", "sc_abi_version",
-                 "sc_block_record_bytes", "sc_tier_pack", "sc_tier_unpack", "sc_prefill_attn"):
+               "sc_block_record_bytes", "sc_tier_pack", "sc_tier_unpack", "sc_prefill_attn", "sc_block_scores",
+               "sc_block_values"):
         assert fn in names
 
 
@@ -36,7 +37,7 @@ def test_library_exports_every_declared_symbol():
     for fn in _declared_functions():
         assert hasattr(lib, fn), fn
     assert set(_lib.PROTOTYPES) == _declared_functions()
-    assert _lib.load().sc_abi_version() == _lib.ABI_VERSION == 5
+    assert _lib.load().sc_abi_version() == _lib.ABI_VERSION == 6
 
 
 def test_struct_layouts_match_header():
@@ -57,3 +58,24 @@ def test_errors_are_reported_without_a_gpu():
     args = _lib.ScDecodeArgs()
     assert lib.sc_decode_attn(ctypes.byref(args), None, 0, None) == -1
     assert b"null" in lib.sc_last_error()
+
+
+def test_host_side_checks_refuse_bad_calls_without_a_gpu():
+    """Argument checks that return before anything is launched."""
+    from unsloth_spectral import _lib
+    lib = _lib.load()
+    tier = _lib.ScTierDesc()
+    assert lib.sc_tier_append(ctypes.byref(tier), None, None, 0, 0, 0, None, 1, 0, None) == -1   # null tier arrays
+    assert lib.sc_tier_append(None, None, None, 0, 0, 0, None, 1, 0, None) == -1
+    buf = ctypes.create_string_buffer(64)
+    for name in ("counters", "tail_k", "tail_v", "tail_pos"):
+        setattr(tier, name, ctypes.addressof(buf))
+    tier.tail_capacity, tier.head_dim = 16, 128
+    assert lib.sc_tier_append(ctypes.byref(tier), None, None, 0, 0, 0, None, 1, 8, None) == -1    # unknown flag
+    assert b"flags" in lib.sc_last_error()
+    assert lib.sc_tier_append(ctypes.byref(tier), None, None, 0, 0, 0, None, 17, 0, None) == -5   # > ring
+    assert lib.sc_block_scores(None, 0, 0, 1, 8, None, None, 2, 16, 8, 128, None, None, 128, 64, 0, None,
+                               None) == -1
+    assert lib.sc_block_values(None, 0, 0, 1, 8, None, None, 3, 16, 8, 128, None, None) == -1    # 8 % 3
+    assert b"multiple" in lib.sc_last_error()
+    assert lib.sc_block_values(None, 0, 0, 1, 8, None, None, 2, 16, 65, 128, None, None) == -2   # rank > 64

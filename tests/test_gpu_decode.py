@@ -278,3 +278,89 @@ def test_empty_cache_raises():
     cos, sin = tables(*rope_tables(16, 128))
     with pytest.raises(ValueError):
         spectral_attention_decode(torch.zeros(1, 8, 1, 128, dtype=torch.float16, device="cuda"), c, cos, sin, 0)
+
+
+# ---------------------------------------------------------------- branch-free path
+# sc_decode_attn runs its branch-free instantiation (the one the benchmark
+# times) when no mask and no logits are requested, RoPE is absolute or
+# distance over a table with equal halves, the KV heads are a multiple of 4
+# and the GQA group holds at most 4 query heads.  These tests ask for no
+# logits, so that path is the one compared with the oracle; the logits of
+# the Pearson check come from a second call with logits (the general path)
+# on the same tiers, whose output is checked as well.
+
+def _check_fast(states, Q16, cos, sin, q, mode, block_size=None, seqs=None, split=0):
+    out, _ = _run(states, Q16, cos, sin, q, mode, block_size=block_size, split=split, with_logits=False)
+    out_g, logits = _run(states, Q16, cos, sin, q, mode, block_size=block_size, split=split, with_logits=True)
+    fn = o_abs if mode == "absolute" else o_dist
+    for b in (seqs if seqs is not None else range(len(states))):
+        ref, _, logits16 = fn(Q16[b], states[b], cos, sin, q)
+        ref = ref.astype(np.float64)
+        for o in (out[b], out_g[b]):
+            err = np.abs(o - ref).max()
+            assert err <= ATOL, (b, err)
+            assert err <= RTOL_MAX * np.abs(ref).max(), (b, err, np.abs(ref).max())
+        assert np.isfinite(logits[b]).all()
+        assert pearson(logits[b], logits16) >= 0.9999, b
+    return out, out_g, logits
+
+
+@pytest.mark.parametrize("mode", ["absolute", "distance"])
+@pytest.mark.parametrize("per_row", [False, True])
+@pytest.mark.parametrize("ranks", [(16, 16), (16, 32), (32, 32)])
+def test_fast_path_modes_scales_ranks(mode, per_row, ranks):
+    """8 KV heads / 32 query heads, 3 blocks of 512 + a 200-token tail, two
+    sequences with different data."""
+    kK, kV = ranks
+    rng = np.random.default_rng(zlib.crc32(repr(("fast", mode, per_row, ranks)).encode()))
+    states = [random_state(rng, 8, 128, 3, 512, kK, kV, 200, per_row=per_row, batched_qr=True) for _ in range(2)]
+    total = states[0].total_tokens()
+    cos, sin = rope_tables(total + 16, 128)
+    Q = rng.standard_normal((2, 32, 128)).astype(np.float16)
+    print(f"fast path mode={mode} per_row={per_row} ranks={ranks}", flush=True)
+    _check_fast(states, Q, cos, sin, total - 1, mode)
+
+
+@pytest.mark.parametrize("per_row", [False, True])
+def test_fast_path_c1_geometry(per_row):
+    """Batch 1, 4096 context: 7 cold blocks k=16 + 512 tail, both modes."""
+    rng = np.random.default_rng(40 + per_row)
+    states = [random_state(rng, 8, 128, 7, 512, 16, 16, 512, per_row=per_row, batched_qr=True)]
+    cos, sin = rope_tables(4096 + 64, 128)
+    Q = rng.standard_normal((1, 32, 128)).astype(np.float16)
+    for mode in ("absolute", "distance"):
+        print(f"C1 fast path per_row={per_row} mode={mode}", flush=True)
+        _check_fast(states, Q, cos, sin, 4095, mode)
+
+
+@pytest.mark.parametrize("mode", ["absolute", "distance"])
+def test_fast_path_c3_geometry(mode):
+    """Batch 8, 16384 context: 31 cold blocks k=32 per row + 512 tail.  Two
+    sequences against the oracle; every other one equals itself decoded
+    alone at the same split (batch invariance)."""
+    rng = np.random.default_rng(50 + (mode == "distance"))
+    states = [random_state(rng, 8, 128, 31, 512, 32, 32, 512, per_row=True, batched_qr=True) for _ in range(8)]
+    cos, sin = rope_tables(16384 + 64, 128)
+    Q = rng.standard_normal((8, 32, 128)).astype(np.float16)
+    print(f"C3 fast path mode={mode}", flush=True)
+    out, _, _ = _check_fast(states, Q, cos, sin, 16383, mode, seqs=[0, 5], split=1)
+    for b in (1, 2, 3, 4, 6, 7):
+        alone, _ = _run([states[b]], Q[b:b + 1], cos, sin, 16383, mode, split=1, with_logits=False)
+        np.testing.assert_array_equal(alone[0], out[b])
+
+
+def test_fast_path_c5_geometry():
+    """Batch 16, 64 cold blocks k=32 (per row) + 512 tail = 33,280 context,
+    absolute RoPE.  Four distinct sequences (each used four times); two
+    compared with the oracle, the rest by batch invariance."""
+    rng = np.random.default_rng(60)
+    distinct = [random_state(rng, 8, 128, 64, 512, 32, 32, 512, per_row=True, batched_qr=True) for _ in range(4)]
+    states = [distinct[b % 4] for b in range(16)]
+    ctx = 64 * 512 + 512
+    cos, sin = rope_tables(ctx + 64, 128)
+    Q = rng.standard_normal((16, 32, 128)).astype(np.float16)
+    print("C5 fast path", flush=True)
+    out, _, _ = _check_fast(states, Q, cos, sin, ctx - 1, "absolute", seqs=[0, 9])
+    for b in (3, 14):
+        alone, _ = _run([states[b]], Q[b:b + 1], cos, sin, ctx - 1, "absolute", split=1, with_logits=False)
+        np.testing.assert_array_equal(alone[0], out[b])

@@ -118,3 +118,76 @@ def test_cold_blocks_and_decode_compression_match_dense_over_tiers():
     print(f"decode kernel vs dense over the reconstruction: {err:.2e}")
     assert err < 1e-2
     assert _same_choice(kernel, dense)
+
+
+def test_left_padded_batch_generation_matches_unpatched_model():
+    """Batched greedy generation with a left-padded prompt (HF generate):
+    the pad keys enter the cache but are never attended (the prompt's mask
+    is kept as the cache's key mask), so the patched model's logits equal
+    the unpatched model's (fp32 weights, fp16 attention on our side)."""
+    from unsloth_spectral import patch_unsloth_attention
+    model = _model(seed=5)
+    n = 60
+    ids = _tokens(2 * n, seed=6).reshape(2, n)
+    am = torch.ones(2, n, dtype=torch.long)
+    am[0, :7] = 0                                   # sequence 0: 7 pad tokens on the left
+    ref_model = _gpu(model, torch.float32)
+    with torch.no_grad():
+        ref = ref_model.generate(ids.cuda(), attention_mask=am.cuda(), max_new_tokens=8, do_sample=False,
+                                 output_logits=True, return_dict_in_generate=True, pad_token_id=0)
+    ref_logits = torch.stack(ref.logits, 1).float()            # [2, 8, V]
+    patch_unsloth_attention(ref_model, verbose=False)
+    with torch.no_grad():
+        got = ref_model.generate(ids.cuda(), attention_mask=am.cuda(), max_new_tokens=8, do_sample=False,
+                                 output_logits=True, return_dict_in_generate=True, pad_token_id=0)
+    got_logits = torch.stack(got.logits, 1).float()
+    for b in range(2):
+        # the two runs feed back their own greedy tokens: compare the steps
+        # up to the first differing token (identical inputs until then),
+        # and accept a differing token only where the reference's top two
+        # logits are closer than twice the logit error
+        same = (got.sequences[b, n:] == ref.sequences[b, n:]).tolist()
+        upto = same.index(False) + 1 if False in same else len(same)
+        err = _rel(got_logits[b, :upto], ref_logits[b, :upto])
+        print(f"sequence {b}: {upto} steps with equal inputs, max |dlogit| / max |logit| = {err:.2e}")
+        assert err < 5e-3, b
+        assert _same_choice(got_logits[b, :upto], ref_logits[b, :upto])
+        assert upto >= 4, b
+    cache = ref_model.model.layers[0].self_attn._spectral_cache
+    assert cache.key_mask is not None and int(cache.key_mask[0, :7].sum()) == 0
+
+
+def test_decode_steps_of_the_patched_attention_do_not_synchronise():
+    """After the prompt (through the whole model), one-token steps through a
+    patched attention module -- the call transformers makes per layer, with
+    position ids on the device and a block compressed on the way -- run
+    under torch's sync debug mode "error": no step waits for the device.
+    (transformers' own mask preparation around the layers reads the device
+    on its own, e.g. masking_utils.eager_mask builds a scalar tensor on the
+    device, so the check is made at the attention module.)"""
+    from unsloth_spectral import patch_unsloth_attention
+    model = _gpu(_model(seed=7))
+    patch_unsloth_attention(model, block_size=128, verbose=False)
+    n_prompt, steps = 120, 12                       # the block boundary at 128 is crossed during decode
+    ids = _tokens(n_prompt, seed=8).cuda()
+    attn = model.model.layers[0].self_attn
+    rotary = model.model.rotary_emb
+    pos_all = torch.arange(n_prompt + steps, device="cuda")[None]
+    g = torch.Generator(device="cuda").manual_seed(9)
+    hidden = torch.randn(steps, 1, 1, model.config.hidden_size, generator=g, device="cuda").half()
+    with torch.no_grad():
+        model(input_ids=ids, position_ids=pos_all[:, :n_prompt], use_cache=False)
+        cos, sin = rotary(hidden[0], pos_all)                  # [1, L, D] tables of the positions
+        torch.cuda.synchronize()
+        torch.cuda.set_sync_debug_mode("error")
+        try:
+            for i in range(steps):
+                p = n_prompt + i
+                out, _ = attn(hidden[i], position_embeddings=(cos[:, p:p + 1], sin[:, p:p + 1]),
+                              attention_mask=None, position_ids=pos_all[:, p:p + 1])
+        finally:
+            torch.cuda.set_sync_debug_mode(0)
+    torch.cuda.synchronize()
+    cache = attn._spectral_cache
+    assert cache.num_cold_blocks == 1 and cache.total_tokens == n_prompt + steps
+    assert torch.isfinite(out).all()

@@ -1,0 +1,77 @@
+"""The model loop at the exact Mistral-7B shape: transformers
+MistralForCausalLM with 32 layers, hidden 4096, 32 query / 8 KV heads of
+dim 128, SwiGLU FFN 14336, vocab 32768, RMSNorm, RoPE theta 1e6, fp16
+weights ~ N(0, 0.02^2) (random init), patched by patch_unsloth_attention with
+k = 16 (integration.py:596-659, 728-889).
+
+An 8192-token prompt of uniform random ids, then 16 one-token steps teacher
+forced with fixed random tokens (so both runs see the same inputs).  The
+logits of the patched model (HIP prefill and decode kernels over the tiers)
+must equal those of the same model patched with use_spectral_attention=False
+(the reference's dense attention over get_kv, integration.py:292-402) within
+1e-2 of max |logit|, at every step.  With an 8190-token prompt the tail
+reaches 512 tokens at the second decode step, so a block is compressed on
+the device during decode."""
+import pytest
+import torch
+
+pytestmark = pytest.mark.gpu
+
+
+@pytest.fixture(scope="module")
+def mistral7b():
+    from transformers import MistralConfig, MistralForCausalLM
+    cfg = MistralConfig(vocab_size=32768, hidden_size=4096, intermediate_size=14336, num_hidden_layers=32,
+                        num_attention_heads=32, num_key_value_heads=8, head_dim=128,
+                        max_position_embeddings=32768, rope_theta=1e6, sliding_window=None, rms_norm_eps=1e-5,
+                        initializer_range=0.02)
+    cfg._attn_implementation = "sdpa"
+    torch.manual_seed(0)
+    with torch.device("cuda"):
+        model = MistralForCausalLM._from_config(cfg, dtype=torch.float16).eval()
+    print("Mistral-7B-shape model built", flush=True)
+    yield model
+    del model
+    torch.cuda.empty_cache()
+
+
+@torch.no_grad()
+def _teacher_forced(model, ids, n_prompt):
+    """Logits after the prompt and after each one-token step ([steps + 1, V])."""
+    from unsloth_spectral.integration import reset_spectral_caches
+    reset_spectral_caches(model)
+    pos = torch.arange(ids.shape[1], device="cuda")[None]
+    out = [model(input_ids=ids[:, :n_prompt], position_ids=pos[:, :n_prompt], use_cache=False,
+                 logits_to_keep=1).logits[0, -1].float()]
+    for p in range(n_prompt, ids.shape[1] - 1):
+        out.append(model(input_ids=ids[:, p:p + 1], position_ids=pos[:, p:p + 1], use_cache=False,
+                         logits_to_keep=1).logits[0, -1].float())
+    return torch.stack(out)
+
+
+@pytest.mark.parametrize("n_prompt", [8192, 8190])
+def test_c4_model_kernels_match_dense_attention_over_tiers(mistral7b, n_prompt):
+    from unsloth_spectral import get_cache_stats, patch_unsloth_attention
+    steps = 16
+    g = torch.Generator().manual_seed(12)
+    ids = torch.randint(0, 32768, (1, n_prompt + steps + 1), generator=g).cuda()
+    patch_unsloth_attention(mistral7b, k_rank_keys=16, k_rank_values=16, verbose=False)
+    kernel = _teacher_forced(mistral7b, ids, n_prompt)
+    st = get_cache_stats(mistral7b)
+    caches = [layer.self_attn._spectral_cache for layer in mistral7b.model.layers]
+    total = n_prompt + steps
+    assert all(c.total_tokens == total and c.num_cold_blocks == total // 512 for c in caches)
+    assert st["total_blocks"] == 32 * (total // 512)
+    compressed_in_decode = total // 512 - n_prompt // 512
+    print(f"prompt {n_prompt}: {total // 512} blocks per layer, {compressed_in_decode} compressed during decode",
+          flush=True)
+    patch_unsloth_attention(mistral7b, k_rank_keys=16, k_rank_values=16, use_spectral_attention=False,
+                            verbose=False)
+    dense = _teacher_forced(mistral7b, ids, n_prompt)
+    scale = dense.abs().max()
+    err = ((kernel - dense).abs().max(dim=-1).values / scale).cpu()
+    print(f"prompt {n_prompt}: max |dlogit| / max |logit| per step: {[round(float(e), 5) for e in err]}", flush=True)
+    assert torch.isfinite(kernel).all() and torch.isfinite(dense).all()
+    assert float(err.max()) < 1e-2
+    if n_prompt == 8190:
+        assert compressed_in_decode == 1

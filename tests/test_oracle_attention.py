@@ -121,3 +121,50 @@ def test_golden_decode_tiny():
     for mode, fn in (("absolute", spectral_attention_decode), ("distance", spectral_attention_forward)):
         out, _, _ = fn(case["Q"], case["state"], case["cos"], case["sin"], case["q"])
         assert np.abs(out.astype(np.float64) - case[f"out64_{mode}"]).max() < 2e-3
+
+
+def test_block_score_restatement_vs_closed_form():
+    """spectral_score_forward: q . R_p(C_t B) in float64 with every key
+    rotated itself at its absolute position p = start + t by the reference's
+    _apply_rope halves (x1 c1 - x2 s1, x2 c2 + x1 s2), against the
+    restatement that inverse-rotates the query instead.  Unequal table
+    halves make a swapped half or a wrong sign fail."""
+    from oracle.attention import spectral_score_forward
+    rng = np.random.default_rng(70)
+    Hkv, rep, T, k, D, start = 2, 4, 96, 16, 128, 300
+    cos, sin = rope_tables(start + T + 4, D)
+    cos = cos.copy()
+    cos[:, D // 2:] = (cos[:, D // 2:].astype(np.float32) * 0.9).astype(np.float16)
+    coeffs = (rng.standard_normal((Hkv, T, k)) * 0.8).astype(np.float16)
+    basis = (rng.standard_normal((Hkv, k, D)) / np.sqrt(D)).astype(np.float16)
+    Q = rng.standard_normal((Hkv * rep, D)).astype(np.float16)
+    got = spectral_score_forward(Q, coeffs, basis, cos, sin, start).astype(np.float64)
+    K = np.matmul(coeffs.astype(np.float64), basis.astype(np.float64))      # [Hkv, T, D]
+    p = np.arange(start, start + T)
+    c, s = cos[p].astype(np.float64), sin[p].astype(np.float64)
+    h = D // 2
+    x1, x2 = K[..., :h], K[..., h:]
+    Kr = np.concatenate([x1 * c[:, :h] - x2 * s[:, :h], x2 * c[:, h:] + x1 * s[:, h:]], axis=-1)
+    ref = np.einsum("hd,htd->ht", Q.astype(np.float64), np.repeat(Kr, rep, axis=0))
+    assert np.abs(got - ref).max() <= 5e-3 * np.abs(ref).max()
+    assert pearson(got, ref) > 0.99999
+
+
+def test_block_value_restatement_vs_closed_form():
+    """spectral_value_forward: float64 P . (C B) with the query head h using
+    KV head h // rep (repeat_interleave), against the restatement's
+    (P . C) . B in fp32."""
+    from oracle.attention import spectral_value_forward
+    rng = np.random.default_rng(71)
+    Hkv, rep, T, k, D = 2, 4, 200, 32, 128
+    coeffs = (rng.standard_normal((Hkv, T, k)) * 0.8).astype(np.float16)
+    basis = (rng.standard_normal((Hkv, k, D)) / np.sqrt(D)).astype(np.float16)
+    P = rng.random((Hkv * rep, T)).astype(np.float32)
+    P /= P.sum(-1, keepdims=True)
+    got = spectral_value_forward(P, coeffs, basis).astype(np.float64)
+    V = np.matmul(coeffs.astype(np.float64), basis.astype(np.float64))
+    ref = np.einsum("ht,htd->hd", P.astype(np.float64), np.repeat(V, rep, axis=0))
+    assert np.abs(got - ref).max() <= 2e-3 * np.abs(ref).max() + 1e-6
+    # head 5 reads KV head 1: using KV head 0 instead is far off
+    wrong = P[5].astype(np.float64) @ V[0]
+    assert np.abs(wrong - ref[5]).max() > 10 * np.abs(got[5] - ref[5]).max()

@@ -108,6 +108,16 @@ __device__ __forceinline__ half8_t i8x8_to_h8(uint2 w) {
 // the surrounding arithmetic from interleaving.
 __device__ __forceinline__ void pin_vmem() { __builtin_amdgcn_sched_barrier(0x40F); }
 
+// Value barrier: the compiler cannot look through it, so the value is
+// rounded to its own type here.  Used where results must be rounded in the
+// reference's order: without it, fptrunc(fmul) and a following add can be
+// fused into one (mixed-precision) FMA with a single rounding.
+template <class T>
+__device__ __forceinline__ T rounded(T x) {
+  asm volatile("" : "+v"(x));
+  return x;
+}
+
 __device__ __forceinline__ half2_t pack_h2(float a, float b) {
   return (half2_t){(h16)a, (h16)b};
 }

@@ -1394,16 +1394,13 @@ extern "C" int sc_decode_workspace_size(const ScDecodeArgs* args, size_t* bytes)
   return SC_OK;
 }
 
-extern "C" int sc_decode_attn(const ScDecodeArgs* args, void* workspace, size_t workspace_bytes_, void* stream) {
-  DecodeParams p;
-  int rc = fill_params(args, &p);
-  if (rc) return rc;
+namespace {
+
+// Launches the partial and combine kernels with the records at ws (of at
+// least workspace_bytes(p) bytes, checked by the caller).
+int decode_launch(const ScDecodeArgs* args, DecodeParams& p, float* ws, void* stream) {
   const int D = args->tier->head_dim;
-  const size_t need = workspace_bytes(p, D);
-  if (!workspace || workspace_bytes_ < need)
-    return sc_fail(SC_ERR_WORKSPACE, "decode workspace too small: %zu < %zu bytes", workspace_bytes_, need);
-  if (p.units_per_bh == 0) return sc_fail(SC_ERR_INVALID, "empty cache: no blocks and no tail scanned");
-  p.ws = (float*)workspace;
+  p.ws = ws;
   p.young_slot = cus_per_xcd();
   hipStream_t s = (hipStream_t)stream;
   const int kk = args->tier->kp_keys, kv = args->tier->kp_values;
@@ -1414,4 +1411,17 @@ extern "C" int sc_decode_attn(const ScDecodeArgs* args, void* workspace, size_t 
   if (D == 128)
     return gen ? dispatch_kk<128, true>(p, kk, kv, s) : dispatch_kk<128, false>(p, kk, kv, s);
   return gen ? dispatch_kk<64, true>(p, kk, kv, s) : dispatch_kk<64, false>(p, kk, kv, s);
+}
+
+}  // namespace
+
+extern "C" int sc_decode_attn(const ScDecodeArgs* args, void* workspace, size_t workspace_bytes_, void* stream) {
+  DecodeParams p;
+  int rc = fill_params(args, &p);
+  if (rc) return rc;
+  const size_t need = workspace_bytes(p, args->tier->head_dim);
+  if (!workspace || workspace_bytes_ < need)
+    return sc_fail(SC_ERR_WORKSPACE, "decode workspace too small: %zu < %zu bytes", workspace_bytes_, need);
+  if (p.units_per_bh == 0) return sc_fail(SC_ERR_INVALID, "empty cache: no blocks and no tail scanned");
+  return decode_launch(args, p, (float*)workspace, stream);
 }

@@ -18,10 +18,21 @@ struct AppendParams {
   long sb, sh, st;
   const int32_t* positions;
   int t_new;
+  int flags;
 };
 
+// New generation: the caller says so (SC_APPEND_RESET), or, with
+// SC_APPEND_DETECT_RESET, the sequence's first new position lies below the
+// next expected one (spectral_cache.py:176-189, compared per sequence here).
 __device__ __forceinline__ bool append_resets(const AppendParams& p, const int32_t* cnt, int b) {
-  return p.positions && cnt[SC_CNT_TOTAL] > 0 && p.positions[(long)b * p.t_new] < cnt[SC_CNT_NEXT_POS];
+  if (p.flags & SC_APPEND_RESET) return true;
+  return (p.flags & SC_APPEND_DETECT_RESET) && p.positions && cnt[SC_CNT_TOTAL] > 0 &&
+         p.positions[(long)b * p.t_new] < cnt[SC_CNT_NEXT_POS];
+}
+
+// The rows fit the ring: tail length after the append <= capacity.
+__device__ __forceinline__ bool append_fits(const AppendParams& p, const int32_t* cnt, bool reset) {
+  return (reset ? 0 : cnt[SC_CNT_TAIL_LEN]) + p.t_new <= p.t.tail_capacity;
 }
 
 // Work item = one 16-byte chunk of one K or V row.
@@ -40,6 +51,7 @@ __global__ __launch_bounds__(kThreads) void append_copy_kernel(AppendParams p) {
   const int h = (int)(rem / p.t_new);
   const int32_t* cnt = p.t.counters + b * SC_NCOUNTERS;
   const bool reset = append_resets(p, cnt, b);
+  if (!append_fits(p, cnt, reset)) return;  // nothing written; the finalize kernel records the status
   const int base_len = reset ? 0 : cnt[SC_CNT_TAIL_LEN];
   const int base_head = reset ? 0 : cnt[SC_CNT_TAIL_HEAD];
   const int slot = (base_head + base_len + tt) % p.t.tail_capacity;
@@ -57,7 +69,12 @@ __global__ void append_finalize_kernel(AppendParams p) {
   const int b = blockIdx.x * blockDim.x + threadIdx.x;
   if (b >= p.t.batch) return;
   int32_t* cnt = p.t.counters + b * SC_NCOUNTERS;
-  if (append_resets(p, cnt, b)) {
+  const bool reset = append_resets(p, cnt, b);
+  if (!append_fits(p, cnt, reset)) {  // ring overflow: counters unchanged, status set
+    cnt[SC_CNT_STATUS] = SC_ERR_CAPACITY;
+    return;
+  }
+  if (reset) {
     for (int i = 0; i < SC_NCOUNTERS; ++i) cnt[i] = 0;
   }
   cnt[SC_CNT_TAIL_LEN] += p.t_new;
@@ -72,7 +89,9 @@ struct DequantParams {
   h16* v_out;
 };
 
-// One thread per output element (b, h, token, d) of K and of V.
+// One thread per output element (b, h, token, d) of K and of V.  The
+// coefficient is rounded twice, as the reference stores it: code * scale to
+// fp32, then to fp16 (spectral_cache.py:404).
 __global__ __launch_bounds__(kThreads) void dequant_kernel(DequantParams p) {
   const ScTierDesc& T = p.t;
   const int D = T.head_dim, TB = T.block_size;
@@ -93,8 +112,8 @@ __global__ __launch_bounds__(kThreads) void dequant_kernel(DequantParams p) {
   const h16* bk = (const h16*)T.basis_k + bhj * (long)D * T.kp_keys + (long)d * T.kp_keys;
   const h16* bv = (const h16*)T.basis_v + bhj * (long)D * T.kp_values + (long)d * T.kp_values;
   float ak = 0.f, av = 0.f;
-  for (int i = 0; i < T.k_keys; ++i) ak += (float)(h16)((float)ck[i] * sk) * (float)bk[i];
-  for (int i = 0; i < T.k_values; ++i) av += (float)(h16)((float)cv[(long)i * TB] * sv) * (float)bv[i];
+  for (int i = 0; i < T.k_keys; ++i) ak += (float)(h16)rounded((float)ck[i] * sk) * (float)bk[i];
+  for (int i = 0; i < T.k_values; ++i) av += (float)(h16)rounded((float)cv[(long)i * TB] * sv) * (float)bv[i];
   p.k_out[idx] = (h16)ak;
   p.v_out[idx] = (h16)av;
 }
@@ -103,10 +122,11 @@ __global__ __launch_bounds__(kThreads) void dequant_kernel(DequantParams p) {
 
 extern "C" int sc_tier_append(const ScTierDesc* t, const void* k_new, const void* v_new, int64_t stride_b,
                               int64_t stride_h, int64_t stride_t, const int32_t* positions, int32_t t_new,
-                              void* stream) {
+                              int32_t flags, void* stream) {
   if (!t || !t->counters || !t->tail_k || !t->tail_v || !t->tail_pos)
     return sc_fail(SC_ERR_INVALID, "sc_tier_append: null tier");
   if (t_new < 0) return sc_fail(SC_ERR_INVALID, "negative t_new");
+  if (flags & ~(SC_APPEND_DETECT_RESET | SC_APPEND_RESET)) return sc_fail(SC_ERR_INVALID, "bad append flags %d", flags);
   if (t_new == 0) return SC_OK;
   if (t_new > t->tail_capacity)
     return sc_fail(SC_ERR_CAPACITY, "append of %d tokens exceeds the tail ring (%d)", t_new, t->tail_capacity);
@@ -123,6 +143,7 @@ extern "C" int sc_tier_append(const ScTierDesc* t, const void* k_new, const void
   p.st = stride_t;
   p.positions = positions;
   p.t_new = t_new;
+  p.flags = flags;
   const long items = (long)t->batch * t->kv_heads * t_new * (t->head_dim / 8) * 2;
   hipStream_t s = (hipStream_t)stream;
   hipLaunchKernelGGL(append_copy_kernel, dim3((unsigned)((items + kThreads - 1) / kThreads)), dim3(kThreads), 0, s, p);

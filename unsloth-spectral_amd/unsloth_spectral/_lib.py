@@ -12,13 +12,15 @@ import torch
 _HERE = os.path.dirname(os.path.abspath(__file__))
 LIB_PATH = os.path.join(_HERE, "libspectral_hip.so")
 
-ABI_VERSION = 5  # SC_ABI_VERSION of include/spectral_hip.h
+ABI_VERSION = 6  # SC_ABI_VERSION of include/spectral_hip.h
 SC_OK = 0
 SC_ROPE_ABSOLUTE, SC_ROPE_DISTANCE, SC_ROPE_NONE = 0, 1, 2
 SC_QUANT_PER_HEAD, SC_QUANT_PER_ROW, SC_QUANT_PER_TENSOR = 0, 1, 2
 SC_CNT_NCOLD, SC_CNT_TAIL_HEAD, SC_CNT_TAIL_LEN, SC_CNT_NEXT_POS = 0, 1, 2, 3
-SC_CNT_TOTAL, SC_CNT_COMPRESSIONS = 4, 5
+SC_CNT_TOTAL, SC_CNT_COMPRESSIONS, SC_CNT_STATUS = 4, 5, 6
 SC_NCOUNTERS = 8
+SC_APPEND_DETECT_RESET, SC_APPEND_RESET = 1, 2
+SC_ERR_CAPACITY = -5
 
 SC_DTYPE = {torch.float16: 0, torch.float32: 1, torch.bfloat16: 2}
 GRANULARITY = {"per_head": SC_QUANT_PER_HEAD, "per_row": SC_QUANT_PER_ROW,
@@ -87,7 +89,8 @@ PROTOTYPES = {
     "sc_decode_attn": (c_i32, [ctypes.POINTER(ScDecodeArgs), c_vp, ctypes.c_size_t, c_vp]),
     "sc_rsvd_compress": (c_i32, [ctypes.POINTER(ScCompressArgs), c_vp]),
     "sc_quantize_int8": (c_i32, [c_vp, c_i64, c_i64, c_i64, c_i32, c_vp, c_vp, c_vp, c_vp]),
-    "sc_tier_append": (c_i32, [ctypes.POINTER(ScTierDesc), c_vp, c_vp, c_i64, c_i64, c_i64, c_vp, c_i32, c_vp]),
+    "sc_tier_append": (c_i32, [ctypes.POINTER(ScTierDesc), c_vp, c_vp, c_i64, c_i64, c_i64, c_vp, c_i32, c_i32,
+                               c_vp]),
     "sc_tier_compress": (c_i32, [ctypes.POINTER(ScTierDesc), c_i32, c_i32, c_i32, c_u64, c_vp]),
     "sc_tier_dequant": (c_i32, [ctypes.POINTER(ScTierDesc), c_i32, c_i32, c_vp, c_vp, c_vp]),
     "sc_prefill_attn": (c_i32, [ctypes.POINTER(ScPrefillArgs), c_vp]),
@@ -95,6 +98,10 @@ PROTOTYPES = {
     "sc_tier_pack": (c_i32, [ctypes.POINTER(ScTierDesc), c_i32, c_i32, c_i32, c_vp, ctypes.c_size_t, c_vp]),
     "sc_tier_unpack": (c_i32, [ctypes.POINTER(ScTierDesc), c_i32, c_i32, c_i32, c_vp, ctypes.c_size_t, c_vp,
                                c_vp]),
+    "sc_block_scores": (c_i32, [c_vp, c_i64, c_i64, c_i32, c_i32, c_vp, c_vp, c_i32, c_i32, c_i32, c_i32, c_vp, c_vp,
+                                c_i64, c_i32, c_i32, c_vp, c_vp]),
+    "sc_block_values": (c_i32, [c_vp, c_i64, c_i64, c_i32, c_i32, c_vp, c_vp, c_i32, c_i32, c_i32, c_i32, c_vp,
+                                c_vp]),
     "sc_last_error": (ctypes.c_char_p, []),
     "sc_abi_version": (c_i32, []),
 }

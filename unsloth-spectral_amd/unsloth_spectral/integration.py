@@ -95,35 +95,53 @@ def _model_rope(module, head_dim):
     return tab
 
 
-def _dense_prefill(q_rot, cache, cos_tab, sin_tab, n_rep, attention_mask, scale, q_pos, rows=1024):
+def _dense_prefill(q_rot, cache, cos_tab, sin_tab, n_rep, key_keep, scale, q_pos, rows=1024):
     """Dense attention over get_kv() with keys rotated at their absolute
-    positions (integration.py:297-346): fp16 scores, additive mask, softmax
-    in fp32 cast back to fp16, fp16 P.V.  Causality comes from the positions
+    positions (integration.py:297-346): fp16 scores, softmax in fp32 cast
+    back to fp16, fp16 P.V.  Causality comes from each sequence's positions
     (key position <= query position), so a prompt appended in several chunks
-    sees the right keys; an additive float mask of matching shape is added
-    as well.  Query rows are processed in slices of ``rows`` to bound the
-    [Hq, rows, L] score buffer.  Both products take contiguous operands."""
+    sees the right keys; ``key_keep`` ([B, L] flags, 1 = attend, or None)
+    drops padding keys.  Query rows are processed in slices of ``rows`` to
+    bound the [Hq, rows, L] score buffer.  Both products take contiguous
+    operands."""
     K, V = cache.get_kv()
-    pos = cache.get_all_positions()
-    K = apply_rope(K, cos_tab[pos][None, None], sin_tab[pos][None, None])
+    pos = cache.positions()                                  # [B, L]
+    K = apply_rope(K, cos_tab[pos][:, None], sin_tab[pos][:, None])
     Kt = _repeat_kv(K, n_rep).transpose(2, 3).contiguous()
     V = _repeat_kv(V, n_rep).contiguous()
-    T, L = q_rot.shape[2], Kt.shape[3]
-    extra = None
-    if attention_mask is not None and attention_mask.dim() == 4 and attention_mask.shape[-1] == L \
-            and attention_mask.shape[-2] >= T and attention_mask.is_floating_point():
-        extra = attention_mask[..., -T:, :]
+    B, T = q_rot.shape[0], q_rot.shape[2]
+    q_pos = q_pos.to(pos.device).reshape(-1, T).expand(B, T)
     out = torch.empty_like(q_rot)
     for r0 in range(0, T, rows):
         r1 = min(T, r0 + rows)
         w = torch.matmul(q_rot[:, :, r0:r1].contiguous(), Kt) * scale
-        keep = pos[None, :] <= q_pos[0, r0:r1, None]
-        w = w.masked_fill(~keep, float("-inf"))
-        if extra is not None:
-            w = w + extra[..., r0:r1, :].to(w.dtype)
+        keep = pos[:, None, :] <= q_pos[:, r0:r1, None]       # [B, rows, L]
+        if key_keep is not None:
+            keep = keep & (key_keep[:, None, :] != 0)
+        w = w.masked_fill(~keep[:, None], float("-inf"))
         p = F.softmax(w, dim=-1, dtype=torch.float32).to(q_rot.dtype)
-        out[:, :, r0:r1] = torch.matmul(p, V)
+        out[:, :, r0:r1] = torch.matmul(torch.nan_to_num(p), V)
     return out
+
+
+def _keep_from_mask(mask, B, T):
+    """Keep flags [B, T] (1 = attend) of the keys of the current call, from
+    the HF attention mask handed to the attention module (4-D [B, 1, q, L]:
+    additive float, 0 = attend, or bool, True = attend; or 2-D [B, L]).  The
+    last query row covers every key of the call (causality lets it see
+    them), and the call's keys are the last T columns.  None when the mask
+    does not have that form."""
+    if mask is None:
+        return None
+    row = mask[:, 0, -1, :] if mask.dim() == 4 else mask if mask.dim() == 2 else None
+    if row is None or row.shape[0] != B or row.shape[-1] < T:
+        return None
+    row = row[:, -T:]
+    if row.dtype == torch.bool:
+        return row.to(torch.uint8)
+    if row.is_floating_point():
+        return (row == 0).to(torch.uint8)
+    return (row != 0).to(torch.uint8)
 
 
 def _cache_for(module, num_kv, head_dim, dtype, device, opts):
@@ -149,25 +167,47 @@ def _attend(self, hidden_states, cos_cur, sin_cur, position_ids, attention_mask,
     k = self.k_proj(hidden_states).view(B, T, Hkv, D).transpose(1, 2)
     v = self.v_proj(hidden_states).view(B, T, Hkv, D).transpose(1, 2)
     cache = _cache_for(self, Hkv, D, hidden_states.dtype, hidden_states.device, opts)
-    if position_ids is None:
-        start = cache.current_position
-        position_ids = torch.arange(start, start + T, device=hidden_states.device)[None].expand(B, T)
     tab = _model_rope(self, D)
     if cos_cur is None:
+        cur = position_ids
+        if cur is None:
+            start = cache.current_position
+            cur = torch.arange(start, start + T, device=hidden_states.device)[None].expand(B, T)
         cos_all, sin_all = tab.get(cache.current_position + T + 1, hidden_states.device)
-        cos_cur, sin_cur = cos_all[position_ids], sin_all[position_ids]
+        cos_cur, sin_cur = cos_all[cur], sin_all[cur]
     q_rot = (q * cos_cur[:, None] + rotate_half(q) * sin_cur[:, None]).to(torch.float16)
-    cache.append(k, v, position_ids)                       # pre-RoPE K (integration.py:618-624)
+    # Padding of a batched prompt (left padding): the HF mask of a
+    # multi-sequence call marks the pad keys.  The cache keeps their flags,
+    # and pad tokens get positions that continue backwards from the first
+    # real token, so every sequence's real tokens are contiguous from the
+    # position the model gave its first real token.
+    # Only multi-token calls are inspected (one host read of the mask, like
+    # the position read of a prefill); decode steps read nothing.
+    keep_new = _keep_from_mask(attention_mask, B, T) if B > 1 and T > 1 else None
+    if keep_new is not None and not bool((keep_new == 0).any()):
+        keep_new = None
+    store_pos = position_ids
+    if keep_new is not None and position_ids is not None:
+        store_pos = position_ids[:, -1:] - torch.arange(T - 1, -1, -1, device=position_ids.device)
+    if T > 1:   # room for the prompt and the decode steps after it: those then allocate nothing
+        cache.reserve(cache.current_position + T + opts.get("reserve_tokens", 4096), batch_size=B)
+    cache.append(k, v, store_pos)                          # pre-RoPE K (integration.py:618-624)
+    if keep_new is not None:
+        cache.record_key_mask(keep_new, cache.total_tokens - T)
     cos_tab, sin_tab = tab.get(cache.current_position + 1, hidden_states.device)
     scale = getattr(self, "scaling", None) or 1.0 / math.sqrt(D)
+    key_keep = cache.key_mask_view()
     if T == 1 and opts["use_spectral_attention"]:
-        qpos = position_ids[:, -1]
-        out = run_decode(q_rot, cache, cos_tab, sin_tab, qpos, None, scale, rope_mode, halves_equal=True)
-    elif opts["use_spectral_attention"] and prefill_supported(cache, Hq) and (B == 1 or attention_mask is None):
-        # causal by positions; a padding mask (batch > 1 with a mask) takes the dense path
-        out = run_prefill(q_rot, cache, cos_tab, sin_tab, position_ids, scale)
+        qpos = position_ids[:, -1] if position_ids is not None else cache.current_position - 1
+        out = run_decode(q_rot, cache, cos_tab, sin_tab, qpos, key_keep, scale, rope_mode, halves_equal=True)
+    elif opts["use_spectral_attention"] and prefill_supported(cache, Hq) and key_keep is None:
+        qp = store_pos if store_pos is not None else \
+            torch.arange(cache.current_position - T, cache.current_position, device=q_rot.device)[None]
+        out = run_prefill(q_rot, cache, cos_tab, sin_tab, qp, scale)
     else:
-        out = _dense_prefill(q_rot, cache, cos_tab, sin_tab, Hq // Hkv, attention_mask, scale, position_ids)
+        qp = store_pos if store_pos is not None else \
+            torch.arange(cache.current_position - T, cache.current_position, device=q_rot.device)[None]
+        out = _dense_prefill(q_rot, cache, cos_tab, sin_tab, Hq // Hkv, key_keep, scale, qp)
     out = out.to(hidden_states.dtype).transpose(1, 2).reshape(B, T, Hq * D)
     return self.o_proj(out), cache
 

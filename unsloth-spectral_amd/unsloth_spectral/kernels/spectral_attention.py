@@ -71,51 +71,65 @@ def spectral_attention_decode(
                       split=config.split_blocks if config is not None else 0)
 
 
-def _one_block_cache(coeffs, basis, start_position, kind, D, B):
-    """A one-block cache (B copies) holding `coeffs` [H, T, k] (reference fp16
-    coefficients) as INT8 codes with scale = max|coeff|/127 per head."""
-    H, T, k = coeffs.shape
-    c = coeffs.float()
-    absmax = torch.clamp(c.abs().amax(dim=(1, 2)), min=1e-8)
-    scale = absmax / 127.0
-    codes = torch.round(c / scale[:, None, None]).to(torch.int8)[None, :, None].expand(B, H, 1, T, k)
-    sc = scale[None, :, None].expand(B, H, 1)
-    bas = basis.to(torch.float16)[None, :, None].expand(B, H, 1, k, D)
-    z_codes = torch.zeros(B, H, 1, T, 16, dtype=torch.int8, device=coeffs.device)
-    z_basis = torch.zeros(B, H, 1, 16, D, dtype=torch.float16, device=coeffs.device)
-    ones = torch.ones(B, H, 1, device=coeffs.device)
-    start = torch.full((B, 1), int(start_position), device=coeffs.device)
-    if kind == "K":
-        return SpectralCache.from_tiers(codes, sc, bas, z_codes, ones, z_basis, start, block_size=T)
-    return SpectralCache.from_tiers(z_codes, ones, z_basis, codes, sc, bas, start, block_size=T)
+def _fp16_rows(t, D):
+    """fp16, contiguous, 16-byte aligned rows (what the block kernels read)."""
+    t = t.to(torch.float16)
+    if not t.is_contiguous() or t.data_ptr() % 16:
+        t = t.contiguous()
+    return t
 
 
 def spectral_score_forward(Q, coeffs_K, basis_K, cos, sin, start_position, query_position,
                            config: Optional[TritonSpectralConfig] = None, use_triton: bool = False):
-    """Raw cold-block scores [B, H_q, 1, T_block] in Q's dtype (:375-541):
-    Q . R_p(coeffs_K @ basis_K) with p = start_position + t.  Coefficients
-    are held as INT8 codes (exact for coefficients produced by the
-    reference quantiser, :481-516)."""
+    """Raw cold-block scores [B, H_q, 1, T_block] (:375-541): Q aligned by
+    the inverse RoPE at each key's absolute position start_position + t,
+    projected on basis_K [H_kv, k, D] in fp32, times coeffs_K [H_kv, T, k]
+    and summed in fp32, rounded to fp16 (sc_block_scores).  ``use_triton``
+    selected the reference's Triton kernel; there is one HIP kernel here.
+    ``query_position`` does not enter the absolute alignment (as in the
+    reference)."""
+    _lib.require_device(Q, "Q")
     B, Hq, _, D = Q.shape
-    T = coeffs_K.shape[1]
-    cache = _one_block_cache(coeffs_K, basis_K, start_position, "K", D, B)
-    logits = torch.empty(B, Hq, T, dtype=torch.float32, device=Q.device)
-    run_decode(Q, cache, cos, sin, query_position, None, 1.0, _lib.SC_ROPE_ABSOLUTE, logits=logits)
-    return logits.to(Q.dtype).unsqueeze(2)
+    Hkv, T, k = coeffs_K.shape
+    if basis_K.shape != (Hkv, k, D):
+        raise ValueError(f"basis_K must be [{Hkv}, {k}, {D}], got {tuple(basis_K.shape)}")
+    q = _fp16_rows(Q.reshape(B, Hq, D), D)
+    ck = _fp16_rows(coeffs_K, D)
+    bk = _fp16_rows(basis_K, D)
+    c16 = cos.to(torch.float16).contiguous()
+    s16 = sin.to(torch.float16).contiguous()
+    scores = torch.empty(B, Hq, T, dtype=torch.float16, device=Q.device)
+    lib = _lib.load()
+    _lib.check(lib.sc_block_scores(_lib.ptr(q), q.stride(0), q.stride(1), B, Hq, _lib.ptr(ck), _lib.ptr(bk), Hkv,
+                                   T, k, D, _lib.ptr(c16), _lib.ptr(s16), c16.stride(0),
+                                   min(c16.shape[0], s16.shape[0]), int(start_position), _lib.ptr(scores),
+                                   _lib.stream_of(Q)))
+    return scores.to(Q.dtype).unsqueeze(2)
 
 
 def spectral_value_forward(attn, coeffs_V, basis_V, D, config: Optional[TritonSpectralConfig] = None,
                            use_triton: bool = False):
-    """(attn @ coeffs_V) @ basis_V per query head with GQA (:544-601), fp32
-    accumulation, result in attn's dtype.  A small per-block helper outside
-    the fused path (the fused kernel applies B_V once per block itself)."""
+    """(attn @ coeffs_V) @ basis_V per query head with GQA (:544-601):
+    attn [B, H_q, 1, T] taken in fp32 as the reference does, both products
+    summed in fp32, result [B, H_q, 1, D] in attn's dtype (sc_block_values).
+    The fused decode kernel applies B_V once per block itself; this is the
+    per-block helper of the reference's API."""
+    _lib.require_device(attn, "attn")
     B, Hq, _, T = attn.shape
-    Hkv = coeffs_V.shape[0]
-    n_rep = Hq // Hkv
-    cv = coeffs_V.float().repeat_interleave(n_rep, dim=0)
-    bv = basis_V.float().repeat_interleave(n_rep, dim=0)
-    v_lat = torch.matmul(attn.float(), cv.unsqueeze(0))
-    return torch.matmul(v_lat, bv.unsqueeze(0)).to(attn.dtype)
+    Hkv, T2, k = coeffs_V.shape
+    if T2 != T or basis_V.shape != (Hkv, k, D):
+        raise ValueError(f"coeffs_V [{Hkv}, {T}, k] and basis_V [{Hkv}, k, {D}] expected, got "
+                         f"{tuple(coeffs_V.shape)} and {tuple(basis_V.shape)}")
+    a = attn.reshape(B, Hq, T).float()
+    if a.stride(-1) != 1:
+        a = a.contiguous()
+    cv = _fp16_rows(coeffs_V, D)
+    bv = _fp16_rows(basis_V, D)
+    out = torch.empty(B, Hq, D, dtype=torch.float16, device=attn.device)
+    lib = _lib.load()
+    _lib.check(lib.sc_block_values(_lib.ptr(a), a.stride(0), a.stride(1), B, Hq, _lib.ptr(cv), _lib.ptr(bv), Hkv, T,
+                                   k, D, _lib.ptr(out), _lib.stream_of(attn)))
+    return out.to(attn.dtype).unsqueeze(2)
 
 
 def spectral_attention_decode_pytorch(Q, cache, cos, sin, query_position, attention_mask=None, scale=None):

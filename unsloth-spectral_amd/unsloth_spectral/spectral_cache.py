@@ -47,6 +47,34 @@ class SpectralBlock:
     start_position: int
 
 
+def _first_position(position_ids, T):
+    """The first new position as a host integer, for the new-generation test
+    (spectral_cache.py:177-189), or None when reading it would cost a
+    device-to-host synchronisation on the decode path.
+
+    Host data (ints, sequences, numpy arrays, CPU tensors) is read directly.
+    A device tensor is read only for a multi-token append (prompt prefill or
+    a chunk of it, where the reference reads it too); a one-token append
+    with device positions is taken to continue the sequence, so a decode
+    step never waits for the device.  A new generation that starts with a
+    one-token prompt is therefore detected only from host positions or by
+    calling ``reset()`` first."""
+    if isinstance(position_ids, int):
+        return position_ids
+    if isinstance(position_ids, torch.Tensor):
+        if position_ids.numel() == 0:
+            return None
+        if position_ids.device.type != "cpu" and T <= 1:
+            return None
+        return int(position_ids.reshape(-1)[0])
+    try:
+        import numpy as np
+        arr = np.asarray(position_ids).reshape(-1)
+        return int(arr[0]) if arr.size else None
+    except (TypeError, ValueError):
+        return None
+
+
 def padded_rank(k):
     """Storage rank of the INT8 codes / bases (zero-padded)."""
     for kp in (16, 32, 64):
@@ -133,6 +161,7 @@ class SpectralCache:
         self._n_cold = 0
         self._tail_len = 0
         self._tail_head = 0
+        self.key_mask = None
 
     def _allocate(self, batch):
         B, H, D, TB, NB, C = batch, self.num_heads, self.head_dim, self.block_size, self._max_blocks, self._tail_cap
@@ -212,6 +241,20 @@ class SpectralCache:
         self._tail_cap = cap
         self._desc = None
 
+    def reserve(self, tokens: int, batch_size: Optional[int] = None):
+        """Sizes the tiers for ``tokens`` tokens per sequence (cold slots for
+        every full block, a ring of at least two blocks), so that appends up
+        to that length allocate nothing: a decode step then neither allocates
+        nor waits for the device.  ``batch_size`` allocates a cache that has
+        not seen an append yet."""
+        if self._B is None:
+            if batch_size is None:
+                raise ValueError("reserve() on an empty cache needs batch_size")
+            self._max_blocks = max(self._max_blocks, tokens // self.block_size)
+            self._allocate(batch_size)
+            return
+        self._grow_cold(tokens // self.block_size)
+
     _BUFFERS = ("codes_k", "codes_v", "scales_k", "scales_v", "minmax_k", "minmax_v", "vnorm", "basis_k",
                 "basis_v", "block_start", "tail_k", "tail_v", "tail_pos", "counters")
 
@@ -221,6 +264,8 @@ class SpectralCache:
         if self._B is not None:
             for name in self._BUFFERS:
                 setattr(c, name, getattr(self, name).clone())
+        if self.key_mask is not None:
+            c.key_mask = self.key_mask.clone()
         c._desc = None
         c.cache_id = id(c)
         return c
@@ -245,11 +290,15 @@ class SpectralCache:
             self._allocate(B)
         elif B != self._B:
             raise ValueError(f"cache holds {self._B} sequences, append has {B}")
+        flags = 0
         if position_ids is not None and self.total_tokens > 0:
-            first = int(position_ids.reshape(-1)[0])           # :177-183
-            if first < self.current_position:
-                self.reset()
+            first = _first_position(position_ids, T)          # :177-183
+            if first is not None and first < self.current_position:
+                self._zero_host()                              # :186-189; counters cleared by the append kernel
+                flags = _lib.SC_APPEND_RESET
         if T == 0:
+            if flags:
+                self.counters.zero_()
             return
         K16 = K_new.to(torch.float16)
         V16 = V_new.to(torch.float16)
@@ -261,12 +310,14 @@ class SpectralCache:
             K16 = K16.contiguous()
         pos = None
         if position_ids is not None:
+            if not isinstance(position_ids, torch.Tensor):
+                position_ids = torch.as_tensor(position_ids)
             pos = position_ids.to(device=self.device, dtype=torch.int32).reshape(-1, T)
             pos = pos.expand(B, T).contiguous() if pos.shape[0] != B else pos.contiguous()
         self._grow_tail(self._tail_len + T)
         st = _lib.stream_of(K16)
         check(_lib.load().sc_tier_append(ctypes.byref(self._tier()), ptr(K16), ptr(V16), K16.stride(0),
-                                         K16.stride(1), K16.stride(2), ptr(pos), T, st))
+                                         K16.stride(1), K16.stride(2), ptr(pos), T, flags, st))
         self.total_tokens += T
         self.current_position += T
         self._tail_len += T
@@ -350,6 +401,50 @@ class SpectralCache:
     def get_spectral_components(self) -> Tuple[List[SpectralBlock], Optional[torch.Tensor], Optional[torch.Tensor]]:
         """spectral_cache.py:518-527"""
         return self.cold_blocks, self.hot_K, self.hot_V
+
+    def positions(self) -> torch.Tensor:
+        """Positions of every cached token of every sequence, [B, L] int64
+        in cache order (cold blocks, then the tail oldest first)."""
+        if self._B is None:
+            return torch.empty(0, 0, dtype=torch.long, device=self.device)
+        parts = []
+        if self._n_cold:
+            ar = torch.arange(self.block_size, device=self.device)
+            parts.append((self.block_start[:, :self._n_cold, None].to(torch.long) + ar).reshape(self._B, -1))
+        if self._tail_len:
+            parts.append(self.tail_pos.index_select(1, self._tail_index()).to(torch.long))
+        if not parts:
+            return torch.empty(self._B, 0, dtype=torch.long, device=self.device)
+        return torch.cat(parts, dim=1)
+
+    # ------------------------------------------------------------ padding (key keep-mask)
+    # Batched generation with left padding: the prompt's pad tokens are
+    # appended like the others, so the cache keeps one keep flag per cached
+    # token (uint8 [B, capacity], 1 = attend) once a padding mask has been
+    # recorded; decode calls pass it as their keep-mask.  The reference's
+    # cache holds one sequence and has no such state.
+    def record_key_mask(self, keep: torch.Tensor, start: int):
+        """Keep flags [B, T] of the tokens at cache indices start .. start+T-1."""
+        T = keep.shape[-1]
+        need = start + T
+        km = self.key_mask
+        if km is None or km.shape[1] < need:
+            cap = max(need, 2 * (km.shape[1] if km is not None else self.block_size))
+            new = torch.ones(self._B, cap, dtype=torch.uint8, device=self.device)
+            if km is not None:
+                new[:, :km.shape[1]] = km
+            self.key_mask = km = new
+        km[:, start:need] = keep.to(torch.uint8)
+
+    def key_mask_view(self) -> Optional[torch.Tensor]:
+        """[B, total] keep flags of the cached tokens, or None without padding."""
+        if self.key_mask is None:
+            return None
+        n = self._n_cold * self.block_size + self._tail_len
+        if self.key_mask.shape[1] < n:
+            self.record_key_mask(torch.ones(self._B, n - self.key_mask.shape[1], dtype=torch.uint8,
+                                            device=self.device), self.key_mask.shape[1])
+        return self.key_mask[:, :n]
 
     def get_all_positions(self) -> torch.Tensor:
         """spectral_cache.py:529-555 (sequence 0)."""
