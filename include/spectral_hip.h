@@ -161,6 +161,20 @@ typedef struct ScDecodeArgs {
 int sc_decode_workspace_size(const ScDecodeArgs* args, size_t* bytes);
 int sc_decode_attn(const ScDecodeArgs* args, void* workspace, size_t workspace_bytes,
                    void* stream);
+/*
+ * sc_decode_attn without a caller workspace and without any allocation.
+ * No counterpart in the reference: it is for callers that cannot allocate
+ * device memory (code under HIP graph capture, tight serving loops,
+ * harnesses that forbid hipMalloc).  The partial records live in a
+ * library-owned device array of SC_DECODE_SCRATCH_BYTES per GPU (held until
+ * the process ends); a call whose records need more (sc_decode_workspace_size)
+ * fails with SC_ERR_WORKSPACE.  Every call on one GPU shares that GPU's
+ * array: calls that overlap in time on one GPU (different streams or host
+ * threads) race and must be serialised by the caller.  Results equal
+ * sc_decode_attn's bit for bit.
+ */
+#define SC_DECODE_SCRATCH_BYTES (32u << 20)
+int sc_decode_attn_noalloc(const ScDecodeArgs* args, void* stream);
 
 
 /*

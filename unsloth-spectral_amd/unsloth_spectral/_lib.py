@@ -21,6 +21,7 @@ SC_CNT_TOTAL, SC_CNT_COMPRESSIONS, SC_CNT_STATUS = 4, 5, 6
 SC_NCOUNTERS = 8
 SC_APPEND_DETECT_RESET, SC_APPEND_RESET = 1, 2
 SC_ERR_CAPACITY = -5
+SC_DECODE_SCRATCH_BYTES = 32 << 20
 
 SC_DTYPE = {torch.float16: 0, torch.float32: 1, torch.bfloat16: 2}
 GRANULARITY = {"per_head": SC_QUANT_PER_HEAD, "per_row": SC_QUANT_PER_ROW,
@@ -87,6 +88,7 @@ class ScCompressArgs(ctypes.Structure):
 PROTOTYPES = {
     "sc_decode_workspace_size": (c_i32, [ctypes.POINTER(ScDecodeArgs), ctypes.POINTER(ctypes.c_size_t)]),
     "sc_decode_attn": (c_i32, [ctypes.POINTER(ScDecodeArgs), c_vp, ctypes.c_size_t, c_vp]),
+    "sc_decode_attn_noalloc": (c_i32, [ctypes.POINTER(ScDecodeArgs), c_vp]),
     "sc_rsvd_compress": (c_i32, [ctypes.POINTER(ScCompressArgs), c_vp]),
     "sc_quantize_int8": (c_i32, [c_vp, c_i64, c_i64, c_i64, c_i32, c_vp, c_vp, c_vp, c_vp]),
     "sc_tier_append": (c_i32, [ctypes.POINTER(ScTierDesc), c_vp, c_vp, c_i64, c_i64, c_i64, c_vp, c_i32, c_i32,
