@@ -259,9 +259,10 @@ def rsvd_rank32_parity(torch, M):
         U, S, Vh = fn(Mn, 32, omega.numpy())
         e = per_matrix_error(Mn, U * S[:, None, :], Vh)
         rel = (e_gpu - e) / e
-        out[name] = {"recon_err": round(float(e.mean()), 6), "rel_diff_mean": round(float(rel.mean()), 6),
-                     "rel_diff_min": round(float(rel.min()), 6), "rel_diff_max": round(float(rel.max()), 6)}
-    out["gpu_recon_err"] = round(float(e_gpu.mean()), 6)
+        sig = lambda x: float(f"{float(x):.3e}")   # noqa: E731  (relative differences are ~1e-7)
+        out[name] = {"recon_err": round(float(e.mean()), 7), "rel_diff_mean": sig(rel.mean()),
+                     "rel_diff_min": sig(rel.min()), "rel_diff_max": sig(rel.max())}
+    out["gpu_recon_err"] = round(float(e_gpu.mean()), 7)
     out["note"] = ("8 blocks 512x128 of the benchmark distribution, one fixed sketch; a negative difference "
                    "means the HIP fit is closer than the oracle's")
     return out
