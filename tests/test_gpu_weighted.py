@@ -169,11 +169,16 @@ def test_landmarks_with_two_sequences():
     H, D, T = 2, 128, 128
     cache = _cache(H, D, T, weighted=False)
     A = torch.from_numpy(rng.standard_normal((2, H, T + 8, D)).astype(np.float16)).cuda()
-    cache.append(A, A)
+    # the two sequences sit at different positions (sequence 1 starts at 1000)
+    start = torch.tensor([[0], [1000]], device="cuda")
+    cache.append(A, A, start + torch.arange(T + 8, device="cuda")[None])
     L = torch.from_numpy(rng.standard_normal((2, H, 1, D)).astype(np.float16)).cuda()
-    cache.add_landmarks(L, L, torch.tensor([[0], [0]], device="cuda"))
+    cache.add_landmarks(L, L, torch.tensor([[0], [7]], device="cuda"))
     K, V, pos = cache.get_kv_with_landmarks()
     assert K.shape == (2, H, 1 + T + 8, D) and pos.shape == (2, 1 + T + 8)
-    assert pos[:, 1:].tolist() == [list(range(T + 8))] * 2
+    assert pos[:, 0].tolist() == [0, 7]
+    assert pos[0, 1:].tolist() == list(range(T + 8))
+    assert pos[1, 1:].tolist() == list(range(1000, 1000 + T + 8))   # cold block of sequence 1, then its tail
+    assert cache.positions().tolist() == pos[:, 1:].tolist()
     Kc, _ = cache.get_kv()
     assert torch.equal(K[:, :, 1:], Kc)

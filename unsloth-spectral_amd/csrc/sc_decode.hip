@@ -650,6 +650,21 @@ __device__ __forceinline__ void range_values(const DecodeParams& p, CB& cb, cons
   }
 }
 
+// A sequence's tier counters, read once at the start of a workgroup into
+// scalar registers: a counter read later, next to the prefetched codes,
+// would make the compiler wait for every load in flight (vmcnt(0)).
+struct SeqCounters {
+  int ncold, tail_head, tail_len;
+};
+__device__ __forceinline__ SeqCounters read_counters(const DecodeParams& p, int b) {
+  const int4 c = *reinterpret_cast<const int4*>(p.counters + b * SC_NCOUNTERS);  // NCOLD, TAIL_HEAD, TAIL_LEN, NEXT_POS
+  SeqCounters s;
+  s.ncold = __builtin_amdgcn_readfirstlane(c.x);
+  s.tail_head = __builtin_amdgcn_readfirstlane(c.y);
+  s.tail_len = __builtin_amdgcn_readfirstlane(c.z);
+  return s;
+}
+
 // Softmax state carried through the tail tiles: running max (log2 domain),
 // lane-partial sum and the accumulated rescale of the cold accumulators.
 struct TailState {
@@ -822,11 +837,10 @@ __device__ __forceinline__ void tail_tile(const DecodeParams& p, int b, int h, i
 // Tail tiles j, j + W, ... (W workgroups per sequence and head group) for a
 // workgroup's wave; `first` holds the already issued loads of tile j.
 template <int D, bool GEN, bool HE>
-__device__ __forceinline__ void tail_tiles(const DecodeParams& p, int b, int h, int j, const half8_t (&qb)[Geo<D>::DS],
-                                           char* vstage, const TailFetch<D>& first, TailState& sm,
-                                           float4_t (&oacc)[Geo<D>::MT]) {
-  const int* cnt = p.counters + b * SC_NCOUNTERS;
-  const int tl = cnt[SC_CNT_TAIL_LEN], th = cnt[SC_CNT_TAIL_HEAD], ncold = cnt[SC_CNT_NCOLD];
+__device__ __forceinline__ void tail_tiles(const DecodeParams& p, const SeqCounters& sc, int b, int h, int j,
+                                           const half8_t (&qb)[Geo<D>::DS], char* vstage, const TailFetch<D>& first,
+                                           TailState& sm, float4_t (&oacc)[Geo<D>::MT]) {
+  const int tl = sc.tail_len, th = sc.tail_head, ncold = sc.ncold;
   const int ntile = (tl + kTile - 1) / kTile;
   h16* vs = reinterpret_cast<h16*>(vstage);
   tail_tile<D, GEN, HE>(p, b, h, j * kTile, tl, ncold, qb, vs, first, sm, oacc);
@@ -891,7 +905,8 @@ __device__ void cold_unit(const DecodeParams& p, int b, int hq, int j, char* sme
   const int nrep = p.nrep;
   const Lanes lr = lane_roles<ONE>(n, nrep);
   const int qhead = ONE ? n >> 2 : n;  // query head of this lane's MFMA column
-  const int ncold = p.counters[b * SC_NCOUNTERS + SC_CNT_NCOLD];
+  const SeqCounters sc = read_counters(p, b);
+  const int ncold = sc.ncold;
   const int jb = j / p.split;                  // cold block of this unit
   const int nR = p.TB / T / p.split;           // ranges of this unit
   const int r0 = (j - jb * p.split) * nR;      // its first range within the block
@@ -912,19 +927,18 @@ __device__ void cold_unit(const DecodeParams& p, int b, int hq, int j, char* sme
 #pragma unroll
     for (int m = 0; m < G::MT; ++m) oacc[m] = (float4_t)0.f;
     const bool he = !GEN || p.halves_equal != 0;
-    const int* cnt = p.counters + b * SC_NCOUNTERS;
-    if (p.fold_tail && j * kTile < cnt[SC_CNT_TAIL_LEN]) {
+    if (p.fold_tail && j * kTile < sc.tail_len) {
       TailFetch<D> tf;
-      tail_fetch<D>(p, b, h, j * kTile, cnt[SC_CNT_TAIL_LEN], cnt[SC_CNT_TAIL_HEAD], true, tf);
+      tail_fetch<D>(p, b, h, j * kTile, sc.tail_len, sc.tail_head, true, tf);
       const bool trope = !GEN || p.rope_mode != SC_ROPE_NONE;
       if (he)
         tail_fetch_rope<D, true>(p, trope, tf);
       else
         tail_fetch_rope<D, false>(p, trope, tf);
       if (he)
-        tail_tiles<D, GEN, true>(p, b, h, j, qt, smem + w * kTile * kVRow * 2, tf, sm, oacc);
+        tail_tiles<D, GEN, true>(p, sc, b, h, j, qt, smem + w * kTile * kVRow * 2, tf, sm, oacc);
       else if constexpr (GEN)
-        tail_tiles<D, GEN, false>(p, b, h, j, qt, smem + w * kTile * kVRow * 2, tf, sm, oacc);
+        tail_tiles<D, GEN, false>(p, sc, b, h, j, qt, smem + w * kTile * kVRow * 2, tf, sm, oacc);
     }
     write_record<D, ONE>(p, b, h, j, lr, oacc, sm.m2, head_sum<ONE>(sm.l));
     return;
@@ -1022,9 +1036,9 @@ __device__ void cold_unit(const DecodeParams& p, int b, int hq, int j, char* sme
   // ranges and the V basis of the final projection during the last one (the
   // basis too would spill registers in the second-to-last)
   TailFetch<D> tf;
-  const int tl = p.counters[b * SC_NCOUNTERS + SC_CNT_TAIL_LEN];
+  const int tl = sc.tail_len;
   const bool has_tail = p.fold_tail && hvalid && j * kTile < tl;
-  tail_fetch<D>(p, b, h, j * kTile, tl, p.counters[b * SC_NCOUNTERS + SC_CNT_TAIL_HEAD], has_tail, tf);
+  tail_fetch<D>(p, b, h, j * kTile, tl, sc.tail_head, has_tail, tf);
   half4_t bvf[G::MT][NT];
   const h16* bvb = p.basis_v + bhj * (long)D * KV;
   auto load_bv = [&]() __attribute__((always_inline)) {
@@ -1058,7 +1072,7 @@ __device__ void cold_unit(const DecodeParams& p, int b, int hq, int j, char* sme
     sm.m2 = st.m2;
     sm.l = st.l;
     sm.scale = 1.f;  // collects the rescale of the cold accumulators
-    tail_tiles<D, GEN, HE>(p, b, h, j, qb, smem + w * kTile * kVRow * 2, tf, sm, oacc);
+    tail_tiles<D, GEN, HE>(p, sc, b, h, j, qb, smem + w * kTile * kVRow * 2, tf, sm, oacc);
     st.m2 = sm.m2;
     st.l = sm.l;
 #pragma unroll

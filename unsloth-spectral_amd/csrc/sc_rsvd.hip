@@ -611,6 +611,31 @@ __device__ __forceinline__ void cholesky_inv_wave(const double* Gs, float* Xf, i
   __syncthreads();
 }
 
+// Columns c < r of Ys [rows][RM] scaled to unit Euclidean norm (a column
+// of zeros stays zero).  Thread t sums column t % RM over rows t / RM,
+// t / RM + G, ... (G = kThreads / RM row groups); the G partial sums of a
+// column are added in a fixed order.  part: >= kThreads floats of scratch.
+template <int RM>
+__device__ __forceinline__ void normalize_cols(float* Ys, int rows, int r, float* part) {
+  constexpr int G = kThreads / RM;
+  const int t = threadIdx.x, c = t % RM, g = t / RM;
+  float s = 0.f;
+  if (g < G && c < r)
+    for (int row = g; row < rows; row += G) s = fmaf(Ys[row * RM + c], Ys[row * RM + c], s);
+  part[t] = s;
+  __syncthreads();
+  if (t < r) {
+    float nn = 0.f;
+    for (int i = 0; i < G; ++i) nn += part[i * RM + t];
+    part[kThreads + t] = nn > 0.f ? 1.0f / sqrtf(nn) : 0.f;
+  }
+  __syncthreads();
+  for (int e = t; e < rows * RM; e += kThreads) {
+    const int cc = e % RM;
+    if (cc < r) Ys[e] *= part[kThreads + cc];
+  }
+}
+
 // Rows of Ys <- rows of Ys X (X upper triangular, fp32 in Xf).  Thread t
 // takes rows t and t + kThreads together (kept in registers), so each
 // float4 of X read from LDS (a broadcast) serves both.  Output columns go
@@ -707,9 +732,11 @@ __device__ __forceinline__ void jacobi_rotation(double app, double aqq, double a
 //      the players of its pairs with PairWalk counters, so the rotation and
 //      element reads go out together; each element has one owner, so the
 //      updates are in place.
-// Stops when the off-diagonal mass is <= 1e-16 of the diagonal mass (the
-// off-diagonal norm below 1e-8 of the diagonal's, far below the fp32 and
-// INT8 rounding of the outputs).
+// Stops when the off-diagonal mass is <= 1e-10 of the diagonal mass (the
+// off-diagonal norm below 1e-5 of the diagonal's): the eigenvectors then
+// mix the retained and the dropped directions by ~1e-5, which moves the
+// reconstruction error of the truncated fit by ~1e-8 relative (second
+// order), far below the fp32 and INT8 rounding of the outputs.
 // scratch: >= 2 * RM / 2 + 2 * kThreads / 64 doubles.
 template <int RM>
 __device__ __forceinline__ void jacobi_eig(double* Gs, double* Ws, double* scratch, int r) {
@@ -762,7 +789,7 @@ __device__ __forceinline__ void jacobi_eig(double* Gs, double* Ws, double* scrat
       off += part[2 * w];
       dia += part[2 * w + 1];
     }
-    if (off <= 1e-16 * dia || dia == 0.0) break;
+    if (off <= 1e-10 * dia || dia == 0.0) break;
     PairWalk wt, wi, wk, wv;
     wt.start(P, t < NPr ? t : 0);
     wi.start(P, mi);
@@ -864,7 +891,21 @@ __device__ __forceinline__ void run_matrix(const RsvdParams& p, const Job& j, in
     }
   };
   mul_m();
-  orth_ys(1);
+  if (n_iter > 0) {
+    // The sketch is only scaled (unit columns; the span is unchanged): that
+    // bounds M^T Y like an orthonormal Y would, so the fp16 hi/lo split of
+    // the next product cannot overflow.  The product of each power
+    // iteration is orthonormalised (one CholeskyQR pass, two for the final
+    // Q, whose second pass restores orthogonality to fp32 rounding when Y is
+    // rank-deficient): the subspace of M M^T applied to an orthonormal Z is
+    // conditioned well enough for fp64 Cholesky, and the fit matches the
+    // float64 subspace iteration with an orthonormalisation after every
+    // product to ~1e-5 of its error.
+    __syncthreads();
+    normalize_cols<RM>(L.Ys, rows, r, L.Zs);  // Zs (the sketch) is dead after M Z
+  } else {
+    orth_ys(2);
+  }
   for (int it = 0; it < n_iter; ++it) {
     __syncthreads();
     mul_mt();
@@ -872,7 +913,6 @@ __device__ __forceinline__ void run_matrix(const RsvdParams& p, const Job& j, in
     mul_m();
     orth_ys(it + 1 == n_iter ? 2 : 1);
   }
-  if (n_iter == 0) orth_ys(1);  // second pass for the final Q
   // ---- Bp^T = M^T Q
   __syncthreads();
   mul_mt();

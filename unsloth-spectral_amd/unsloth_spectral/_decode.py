@@ -20,15 +20,22 @@ _halves = {}
 
 
 def _halves_equal(cos, sin):
+    """Whether both tables have equal halves (HF tables are cat(freqs,
+    freqs)); checked once per table pair and version.  The cache entry holds
+    weak references to the tables: an entry is used only while both of its
+    tables are alive and are the very tensors asked about, so a new table
+    that reuses a freed table's memory is checked afresh."""
+    import weakref
     key = (cos.data_ptr(), sin.data_ptr(), tuple(cos.shape), cos._version, sin._version)
     hit = _halves.get(key)
-    if hit is None:
-        h = cos.shape[-1] // 2
-        hit = bool(torch.equal(cos[:, :h], cos[:, h:]) and torch.equal(sin[:, :h], sin[:, h:]))
-        if len(_halves) > 64:
-            _halves.clear()
-        _halves[key] = hit
-    return hit
+    if hit is not None and hit[0]() is cos and hit[1]() is sin:
+        return hit[2]
+    h = cos.shape[-1] // 2
+    eq = bool(torch.equal(cos[:, :h], cos[:, h:]) and torch.equal(sin[:, :h], sin[:, h:]))
+    if len(_halves) > 64:
+        _halves.clear()
+    _halves[key] = (weakref.ref(cos), weakref.ref(sin), eq)
+    return eq
 
 
 def _as_table(t, D):
