@@ -140,9 +140,10 @@ __device__ __forceinline__ float2 gauss2(unsigned long long seed, unsigned long 
 // ------------------------------------------------------- block helpers
 template <int RM>
 struct Lds {
-  float* Ys;     // [kMaxRows][RM]  Y / Q rows, later Vh [RM][cols]
-  float* Zs;     // [128][RM]       Z / Bp^T
+  float* Ys;     // [kMaxRows][RM]  Y / Q rows, later the coefficient rows
+  float* Zs;     // [128][RM]       Z / Bp^T, later Vh [RM][cols]
   double* Gs;    // [RM][RM]
+  double* G2;    // [RM][RM]        second buffer of the Jacobi iteration
   double* Ws;    // [RM][RM]        eigenvectors
   float* Wf;     // [RM][RM]        W[:, ord] * S for the coefficient product
   double* red;   // [128]
@@ -155,6 +156,8 @@ __device__ Lds<RM> carve(void* base) {
   Lds<RM> l;
   char* p = (char*)base;
   l.Gs = (double*)p;
+  p += sizeof(double) * RM * RM;
+  l.G2 = (double*)p;
   p += sizeof(double) * RM * RM;
   l.Ws = (double*)p;
   p += sizeof(double) * RM * RM;
@@ -174,7 +177,7 @@ __device__ Lds<RM> carve(void* base) {
 
 template <int RM>
 constexpr size_t lds_bytes() {
-  return sizeof(double) * (2 * RM * RM + 128) + sizeof(float) * (kMaxRows * RM + 128 * RM + RM * RM) +
+  return sizeof(double) * (3 * RM * RM + 128) + sizeof(float) * (kMaxRows * RM + 128 * RM + RM * RM) +
          sizeof(int) * (2 * RM + 4);
 }
 
@@ -526,12 +529,6 @@ __device__ __forceinline__ void wave_sync() {
   __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
 }
 
-// Reciprocal to full double precision: hardware estimate + two Newton steps.
-__device__ __forceinline__ double rcp64(double x) {
-  double y = __builtin_amdgcn_rcp(x);
-  y = fma(y, fma(-x, y, 1.0), y);
-  return fma(y, fma(-x, y, 1.0), y);
-}
 __device__ __forceinline__ double rsqrt64(double x) {
   double y = __builtin_amdgcn_rsq(x);
   y = y * fma(-0.5 * x * y, y, 1.5);
@@ -699,74 +696,97 @@ struct PairWalk {
   }
 };
 
-// Jacobi rotation (c, s) that zeroes G[p][q]: tau in fp64 (scale-free), the
-// angle in fp32, then (c, s) renormalised in fp64 by one Newton step, so
-// c^2 + s^2 = 1 to ~1e-14.  An fp32 angle leaves ~1e-7 of G[p][q] behind,
-// which the next sweep removes.
+// Jacobi rotation (c, s) that zeroes G[p][q], branch-free: tau in fp64
+// (scale-free; one Newton step on the reciprocal estimate is ample for the
+// fp32 angle), the angle in fp32, then (c, s) renormalised in fp64 by one
+// Newton step, so c^2 + s^2 = 1 to ~1e-14.  apq = 0 (tau inf or NaN) gives
+// the identity.  An fp32 angle leaves ~1e-7 of G[p][q] behind, which the
+// next sweep removes.
 __device__ __forceinline__ void jacobi_rotation(double app, double aqq, double apq, double& c, double& sn) {
-  c = 1.0;
-  sn = 0.0;
-  if (apq != 0.0) {
-    const float tau = (float)((aqq - app) * rcp64(2.0 * apq));
-    const float at = fabsf(tau);
-    const float tt = at > 1e18f ? __builtin_amdgcn_rcpf(2.0f * tau)
-                                : copysignf(__builtin_amdgcn_rcpf(at + __builtin_amdgcn_sqrtf(fmaf(tau, tau, 1.0f))), tau);
-    const float c32 = __builtin_amdgcn_rsqf(fmaf(tt, tt, 1.0f));
-    const double cd = (double)c32, sd = (double)(tt * c32);
-    const double f = fma(-0.5, fma(cd, cd, sd * sd), 1.5);
-    c = cd * f;
-    sn = sd * f;
-  }
+  const double d2 = 2.0 * apq;
+  double y = __builtin_amdgcn_rcp(d2);
+  y = fma(y, fma(-d2, y, 1.0), y);
+  const float tau = (float)((aqq - app) * y);
+  const float at = fabsf(tau);
+  const float t_mid = copysignf(__builtin_amdgcn_rcpf(at + __builtin_amdgcn_sqrtf(fmaf(tau, tau, 1.0f))), tau);
+  const float t_big = __builtin_amdgcn_rcpf(2.0f * tau);
+  float tt = at > 1e18f ? t_big : t_mid;
+  tt = apq != 0.0 ? tt : 0.0f;
+  const float c32 = __builtin_amdgcn_rsqf(fmaf(tt, tt, 1.0f));
+  const double cd = (double)c32, sd = (double)(tt * c32);
+  const double f = fma(-0.5, fma(cd, cd, sd * sd), 1.5);
+  c = cd * f;
+  sn = sd * f;
+}
+
+// Lane `src`'s double (src < 64, per lane), through the LDS crossbar; all
+// lanes must be active.
+__device__ __forceinline__ double lane_fetch(double v, int src) {
+  const long long u = __double_as_longlong(v);
+  const int lo = __builtin_amdgcn_ds_bpermute(src << 2, (int)(u & 0xffffffffLL));
+  const int hi = __builtin_amdgcn_ds_bpermute(src << 2, (int)(u >> 32));
+  return __longlong_as_double(((long long)hi << 32) | (unsigned)lo);
 }
 
 // Cyclic parallel Jacobi on the symmetric Gs by the whole workgroup:
 // Gs -> diagonal, Ws = eigenvectors.  The round-robin pairing runs over the
 // P = r rounded up to even players (P - 1 rounds per sweep); rows and
 // columns >= r are zeroed first, so a padded player's rotations are the
-// identity.  One round is two barrier-separated phases:
-//   1. NP = P/2 threads compute the rotation (c, s) of one pair each;
-//   2. thread i < NB rotates the 2x2 block (pair mi, pair mk), mi <= mk, of
-//      Gs from both sides (Gs <- J^T Gs J) and writes its mirror; thread t
-//      rotates rows t / NP, t / NP + cnt, ... of pair t % NP of Ws from the
-//      right (cnt = number of threads with that pair).  Each thread walks
-//      the players of its pairs with PairWalk counters, so the rotation and
-//      element reads go out together; each element has one owner, so the
-//      updates are in place.
-// Stops when the off-diagonal mass is <= 1e-10 of the diagonal mass (the
-// off-diagonal norm below 1e-5 of the diagonal's): the eigenvectors then
-// mix the retained and the dropped directions by ~1e-5, which moves the
-// reconstruction error of the truncated fit by ~1e-8 relative (second
-// order), far below the fp32 and INT8 rounding of the outputs.
-// scratch: >= 2 * RM / 2 + 2 * kThreads / 64 doubles.
+// identity.  The matrix is double-buffered (Gs, G2), so a round is one
+// barrier-separated step.  In it every thread first issues all its reads
+// of the current buffer, then:
+//   * each wave computes the rotations (c, s) of all the round's pairs, lane
+//     l taking pair l % NP (every wave computes the same values from the
+//     same entries), and each lane fetches the rotations it needs from the
+//     lanes of its own wave (ds_bpermute: no LDS traffic, no barrier);
+//   * thread i < NB rotates the 2x2 block (pair mi, pair mk), mi <= mk, from
+//     both sides (G <- J^T G J) into the other buffer, with its mirror;
+//   * thread t rotates rows t / NP, t / NP + cnt, ... of pair t % NP of Ws
+//     from the right, in place (cnt = number of threads with that pair).
+// The pairs of a round partition the players, so the blocks cover the
+// P x P matrix once.  Each thread walks the players of its pairs with
+// PairWalk counters.  Stops when the off-diagonal mass is <= 1e-10 of the
+// diagonal mass (the off-diagonal norm below 1e-5 of the diagonal's): the
+// eigenvectors then mix the retained and the dropped directions by ~1e-5,
+// which moves the reconstruction error of the truncated fit by ~1e-8
+// relative (second order), far below the fp32 and INT8 rounding of the
+// outputs.  On return the diagonal of Gs holds the eigenvalues (its other
+// entries, and G2, are garbage).
+// scratch: >= 2 * kThreads / 64 doubles.
 template <int RM>
-__device__ __forceinline__ void jacobi_eig(double* Gs, double* Ws, double* scratch, int r) {
+__device__ __forceinline__ void jacobi_eig(double* Gs, double* G2, double* Ws, double* scratch, int r) {
   static_assert(RM % 2 == 0, "even player count");
   constexpr int NP = RM / 2;
   constexpr int NB = NP * (NP + 1) / 2;  // upper-triangular 2x2 blocks
   constexpr int NW = kThreads / 64;
-  static_assert(NB <= kThreads && 2 * NP + 2 * NW <= 128, "one block per thread; scratch holds 128 doubles");
-  const int t = threadIdx.x;
+  constexpr int WR = (RM + kThreads / NP - 1) / (kThreads / NP);  // Ws rows per thread, at most
+  static_assert(NB <= kThreads && NP <= 64 && 2 * NW <= 128, "one block per thread; one pair per lane");
+  const int t = threadIdx.x, lane = t & 63;
   const int P = r + (r & 1), NPr = P / 2, NBr = NPr * (NPr + 1) / 2;
-  double* rot = scratch;            // [NP][2] = (c, s)
-  double* part = scratch + 2 * NP;  // [NW][2] partial sums
+  double* part = scratch;  // [NW][2] partial sums
   for (int e = t; e < RM * RM; e += kThreads) {
     const int i = e / RM, k = e % RM;
     Ws[e] = (i == k) ? 1.0 : 0.0;
     if (i >= r || k >= r) Gs[e] = 0.0;
+    G2[e] = 0.0;
   }
+  const bool blk = t < NBr;
   int mi = 0, mk = 0;
-  if (t < NBr) {
+  if (blk) {
     mk = (int)((sqrtf(8.0f * (float)t + 1.0f) - 1.0f) * 0.5f);  // t = mk (mk + 1) / 2 + mi
     if ((mk + 1) * (mk + 2) / 2 <= t) ++mk;
     if (mk * (mk + 1) / 2 > t) --mk;
     mi = t - mk * (mk + 1) / 2;
   }
-  const int mv = t % NPr, vcnt = (kThreads - mv + NPr - 1) / NPr;
+  const int mv = t % NPr, vcnt = (kThreads - mv + NPr - 1) / NPr, vrow = t / NPr;
+  const int mr = lane % NPr;
+  double* cur = Gs;
+  double* nxt = G2;
   __syncthreads();
   for (int sweep = 0; sweep < 30; ++sweep) {
     double off = 0.0, dia = 0.0;
     for (int e = t; e < RM * RM; e += kThreads) {
-      const double v = Gs[e];
+      const double v = cur[e];
       if (e / RM == e % RM)
         dia += v * v;
       else
@@ -790,55 +810,74 @@ __device__ __forceinline__ void jacobi_eig(double* Gs, double* Ws, double* scrat
       dia += part[2 * w + 1];
     }
     if (off <= 1e-10 * dia || dia == 0.0) break;
-    PairWalk wt, wi, wk, wv;
-    wt.start(P, t < NPr ? t : 0);
+    PairWalk wr, wi, wk, wv;
+    wr.start(P, mr);
     wi.start(P, mi);
     wk.start(P, mk);
     wv.start(P, mv);
-    for (int step = 0; step < P - 1; ++step, wt.next(), wi.next(), wk.next(), wv.next()) {
-      if (t < NPr) {
-        int pp, qq;
-        wt.players(pp, qq);
-        double c, sn;
-        jacobi_rotation(Gs[pp * RM + pp], Gs[qq * RM + qq], Gs[pp * RM + qq], c, sn);
-        rot[2 * t] = c;
-        rot[2 * t + 1] = sn;
+    for (int step = 0; step < P - 1; ++step, wr.next(), wi.next(), wk.next(), wv.next()) {
+      // all reads of the current buffer first
+      int pr, qr, pi, qi, pk, qk, pm, qm;
+      wr.players(pr, qr);
+      wi.players(pi, qi);
+      wk.players(pk, qk);
+      wv.players(pm, qm);
+      const double app = cur[__umul24(pr, RM) + pr], aqq = cur[__umul24(qr, RM) + qr];
+      const double apq = cur[__umul24(pr, RM) + qr];
+      double a00 = 0.0, a01 = 0.0, a10 = 0.0, a11 = 0.0;
+      if (blk) {
+        a00 = cur[__umul24(pi, RM) + pk];
+        a01 = cur[__umul24(pi, RM) + qk];
+        a10 = cur[__umul24(qi, RM) + pk];
+        a11 = cur[__umul24(qi, RM) + qk];
       }
-      __syncthreads();
-      if (t < NBr) {
-        int pi, qi, pk, qk;
-        wi.players(pi, qi);
-        wk.players(pk, qk);
-        const double ci = rot[2 * mi], si = rot[2 * mi + 1], ck = rot[2 * mk], sk = rot[2 * mk + 1];
-        const double a00 = Gs[pi * RM + pk], a01 = Gs[pi * RM + qk];
-        const double a10 = Gs[qi * RM + pk], a11 = Gs[qi * RM + qk];
+      double vp[WR], vq[WR];
+#pragma unroll
+      for (int jr = 0; jr < WR; ++jr) {
+        const int c = vrow + jr * vcnt;
+        vp[jr] = vq[jr] = 0.0;
+        if (c < P) {
+          vp[jr] = Ws[__umul24(c, RM) + pm];
+          vq[jr] = Ws[__umul24(c, RM) + qm];
+        }
+      }
+      double c0, s0;
+      jacobi_rotation(app, aqq, apq, c0, s0);
+      const double ci = lane_fetch(c0, mi), si = lane_fetch(s0, mi);
+      const double ck = lane_fetch(c0, mk), sk = lane_fetch(s0, mk);
+      const double cm = lane_fetch(c0, mv), sm = lane_fetch(s0, mv);
+      if (blk) {
         const double b00 = ci * a00 - si * a10, b01 = ci * a01 - si * a11;  // rows: J^T A
         const double b10 = si * a00 + ci * a10, b11 = si * a01 + ci * a11;
         const double n00 = ck * b00 - sk * b01, n01 = sk * b00 + ck * b01;  // columns: (J^T A) J
         const double n10 = ck * b10 - sk * b11, n11 = sk * b10 + ck * b11;
-        Gs[pi * RM + pk] = n00;
-        Gs[pi * RM + qk] = n01;
-        Gs[qi * RM + pk] = n10;
-        Gs[qi * RM + qk] = n11;
+        nxt[__umul24(pi, RM) + pk] = n00;
+        nxt[__umul24(pi, RM) + qk] = n01;
+        nxt[__umul24(qi, RM) + pk] = n10;
+        nxt[__umul24(qi, RM) + qk] = n11;
         if (mi != mk) {
-          Gs[pk * RM + pi] = n00;
-          Gs[qk * RM + pi] = n01;
-          Gs[pk * RM + qi] = n10;
-          Gs[qk * RM + qi] = n11;
+          nxt[__umul24(pk, RM) + pi] = n00;
+          nxt[__umul24(qk, RM) + pi] = n01;
+          nxt[__umul24(pk, RM) + qi] = n10;
+          nxt[__umul24(qk, RM) + qi] = n11;
         }
       }
-      {
-        int pm, qm;
-        wv.players(pm, qm);
-        const double cm = rot[2 * mv], sm = rot[2 * mv + 1];
-        for (int c = t / NPr; c < P; c += vcnt) {
-          const double vp = Ws[c * RM + pm], vq = Ws[c * RM + qm];
-          Ws[c * RM + pm] = cm * vp - sm * vq;
-          Ws[c * RM + qm] = sm * vp + cm * vq;
+#pragma unroll
+      for (int jr = 0; jr < WR; ++jr) {
+        const int c = vrow + jr * vcnt;
+        if (c < P) {
+          Ws[__umul24(c, RM) + pm] = cm * vp[jr] - sm * vq[jr];
+          Ws[__umul24(c, RM) + qm] = sm * vp[jr] + cm * vq[jr];
         }
       }
       __syncthreads();
+      double* tmp = cur;
+      cur = nxt;
+      nxt = tmp;
     }
+  }
+  if (cur != Gs) {  // uniform: every thread ran the same rounds
+    for (int e = t; e < RM; e += kThreads) Gs[e * RM + e] = cur[e * RM + e];
   }
   __syncthreads();
 }
@@ -919,7 +958,7 @@ __device__ __forceinline__ void run_matrix(const RsvdParams& p, const Job& j, in
   __syncthreads();
   gram_mfma<RM>(L.Zs, cols, r, L.Gs);  // Bp Bp^T
   __syncthreads();
-  jacobi_eig<RM>(L.Gs, L.Ws, L.red, r);
+  jacobi_eig<RM>(L.Gs, L.G2, L.Ws, L.red, r);
   // ---- eigenvalues in descending order: lane c takes rank = #{larger, or equal with lower index}
   if (t < r) {
     const double lc = L.Gs[t * RM + t];
@@ -942,43 +981,63 @@ __device__ __forceinline__ void run_matrix(const RsvdParams& p, const Job& j, in
     L.Wf[e] = v;
   }
   __syncthreads();
-  // ---- coefficients of my rows (Q in Ys): coeff[i] = sum_c Q[row][c] Wf[c][i];
-  // c runs in a runtime loop and Wf rows are read as float4 broadcasts
+  // ---- coefficients, in place over the Q rows of Ys: Ys[row][i] =
+  // sum_c Q[row][c] Wf[c][i] (0 for k <= i < RM), divided by the row weight
+  // when weighted.  Thread t reads and overwrites only its own rows t and
+  // t + kThreads; c runs in a runtime loop and each float4 of Wf (a wave
+  // broadcast) serves both rows.
   const bool v0 = t < rows, v1 = t + kThreads < rows;
-  float cf0[RM], cf1[RM];
+  {
+    float cf0[RM], cf1[RM];
 #pragma unroll
-  for (int i = 0; i < RM; ++i) cf0[i] = cf1[i] = 0.f;
+    for (int i = 0; i < RM; ++i) cf0[i] = cf1[i] = 0.f;
 #pragma unroll 1
-  for (int c = 0; c < r; ++c) {
-    const float q0 = v0 ? L.Ys[t * RM + c] : 0.f, q1 = v1 ? L.Ys[(t + kThreads) * RM + c] : 0.f;
+    for (int c = 0; c < r; ++c) {
+      const float q0 = v0 ? L.Ys[t * RM + c] : 0.f, q1 = v1 ? L.Ys[(t + kThreads) * RM + c] : 0.f;
 #pragma unroll
-    for (int i = 0; i < RM; i += 4) {
-      if (i < k) {
-        const float4 w = *reinterpret_cast<const float4*>(L.Wf + c * RM + i);
-        cf0[i] = fmaf(q0, w.x, cf0[i]);
-        cf0[i + 1] = fmaf(q0, w.y, cf0[i + 1]);
-        cf0[i + 2] = fmaf(q0, w.z, cf0[i + 2]);
-        cf0[i + 3] = fmaf(q0, w.w, cf0[i + 3]);
-        cf1[i] = fmaf(q1, w.x, cf1[i]);
-        cf1[i + 1] = fmaf(q1, w.y, cf1[i + 1]);
-        cf1[i + 2] = fmaf(q1, w.z, cf1[i + 2]);
-        cf1[i + 3] = fmaf(q1, w.w, cf1[i + 3]);
+      for (int i = 0; i < RM; i += 4) {
+        if (i < k) {
+          const float4 w = *reinterpret_cast<const float4*>(L.Wf + c * RM + i);
+          cf0[i] = fmaf(q0, w.x, cf0[i]);
+          cf0[i + 1] = fmaf(q0, w.y, cf0[i + 1]);
+          cf0[i + 2] = fmaf(q0, w.z, cf0[i + 2]);
+          cf0[i + 3] = fmaf(q0, w.w, cf0[i + 3]);
+          cf1[i] = fmaf(q1, w.x, cf1[i]);
+          cf1[i + 1] = fmaf(q1, w.y, cf1[i + 1]);
+          cf1[i + 2] = fmaf(q1, w.z, cf1[i + 2]);
+          cf1[i + 3] = fmaf(q1, w.w, cf1[i + 3]);
+        }
       }
     }
-  }
-  if (j.rw) {  // undo the row weighting: coeffs / W (spectral_cache.py:389-393)
-    const float w0 = v0 ? row_weight(j, t) : 1.f, w1 = v1 ? row_weight(j, t + kThreads) : 1.f;
+    if (j.rw) {  // undo the row weighting: coeffs / W (spectral_cache.py:389-393)
+      const float w0 = v0 ? row_weight(j, t) : 1.f, w1 = v1 ? row_weight(j, t + kThreads) : 1.f;
 #pragma unroll
-    for (int i = 0; i < RM; ++i)
-      if (i < k) {
-        cf0[i] = cf0[i] / w0;
-        cf1[i] = cf1[i] / w1;
-      }
+      for (int i = 0; i < RM; ++i)
+        if (i < k) {
+          cf0[i] = cf0[i] / w0;
+          cf1[i] = cf1[i] / w1;
+        }
+    }
+    // Wf[c][i] = 0 for i >= k, so cf[i] = 0 there: whole rows are stored
+#pragma unroll
+    for (int i = 0; i < RM; i += 4) {
+      if (v0) *reinterpret_cast<float4*>(L.Ys + t * RM + i) = make_float4(cf0[i], cf0[i + 1], cf0[i + 2], cf0[i + 3]);
+      if (v1)
+        *reinterpret_cast<float4*>(L.Ys + (t + kThreads) * RM + i) =
+            make_float4(cf1[i], cf1[i + 1], cf1[i + 2], cf1[i + 3]);
+    }
   }
-  __syncthreads();  // Q no longer needed: Ys is reused for Vh
-  // Vh (unnormalised) into Ys as [k][cols]: Vh_i[d] = sum_c W[c][ord_i] Bp^T[d][c].
-  // Thread t owns column d = t % cols (its Bp^T row in registers) and ranks
-  // t / cols, t / cols + kThreads / cols, ...; W reads are wave broadcasts.
+  if (p.coeffs_out && dbg_index >= 0) {
+    for (int i = 0; i < k; ++i) {
+      if (v0) p.coeffs_out[(dbg_index * rows + t) * k + i] = L.Ys[t * RM + i];
+      if (v1) p.coeffs_out[(dbg_index * rows + t + kThreads) * k + i] = L.Ys[(t + kThreads) * RM + i];
+    }
+  }
+  // Vh (unnormalised), in place over Bp^T in Zs, as [k][cols]:
+  // Vh_i[d] = sum_c W[c][ord_i] Bp^T[d][c].  Thread t owns column d = t % cols:
+  // it loads its Bp^T row into registers before the barrier, then writes
+  // ranks t / cols, t / cols + kThreads / cols, ...; W reads are wave
+  // broadcasts.  (k cols <= 128 RM: Vh fits in Zs.)
   {
     const int d = t % cols, istep = kThreads / cols;
     float z[RM];
@@ -990,6 +1049,7 @@ __device__ __forceinline__ void run_matrix(const RsvdParams& p, const Job& j, in
       z[c + 2] = z4.z;
       z[c + 3] = z4.w;
     }
+    __syncthreads();  // every Bp^T row is in registers
 #pragma unroll 2
     for (int i = t / cols; i < k; i += istep) {
       const int oi = L.ord[i];
@@ -999,14 +1059,14 @@ __device__ __forceinline__ void run_matrix(const RsvdParams& p, const Job& j, in
         if (c < r) a0 = fma(L.Ws[c * RM + oi], (double)z[c], a0);
         if (c + 1 < r) a1 = fma(L.Ws[(c + 1) * RM + oi], (double)z[c + 1], a1);
       }
-      L.Ys[i * cols + d] = (float)(a0 + a1);
+      L.Zs[i * cols + d] = (float)(a0 + a1);
     }
   }
   __syncthreads();
   for (int i = t >> 6; i < k; i += kThreads / 64) {  // row norms -> 1/norm (0 for vanished rows), one wave per row
     double nn = 0.0;
     for (int d = t & 63; d < cols; d += 64) {
-      const double v = L.Ys[i * cols + d];
+      const double v = L.Zs[i * cols + d];
       nn += v * v;
     }
 #pragma unroll
@@ -1023,35 +1083,34 @@ __device__ __forceinline__ void run_matrix(const RsvdParams& p, const Job& j, in
   // basis
   for (int e = t; e < j.kp * cols; e += kThreads) {
     const int i = e / cols, d = e % cols;
-    const float v = i < k ? (float)(L.Ys[i * cols + d] * L.red[i]) : 0.f;
+    const float v = i < k ? (float)(L.Zs[i * cols + d] * L.red[i]) : 0.f;
     if (j.basis_dmajor)
       j.basis[(long)d * j.kp + i] = (h16)v;
     else
       j.basis[(long)i * cols + d] = (h16)v;
     if (p.vh_out && dbg_index >= 0 && i < k) p.vh_out[(dbg_index * k + i) * cols + d] = v;
   }
-  if (p.coeffs_out && dbg_index >= 0) {
-    for (int i = 0; i < k; ++i) {
-      if (v0) p.coeffs_out[(dbg_index * rows + t) * k + i] = cf0[i];
-      if (v1) p.coeffs_out[(dbg_index * rows + t + kThreads) * k + i] = cf1[i];
-    }
-  }
-  // ---- quantise (spectral_cache.py:481-516 formula)
+  // ---- quantise (spectral_cache.py:481-516 formula); each thread re-reads
+  // its own coefficient rows from Ys
   float am0 = 0.f, am1 = 0.f, mn = INFINITY, mx = -INFINITY;
+  auto row_stats = [&](int row, float& am) __attribute__((always_inline)) {
 #pragma unroll
-  for (int i = 0; i < RM; ++i)
-    if (i < k) {
-      if (v0) {
-        am0 = fmaxf(am0, fabsf(cf0[i]));
-        mn = fminf(mn, cf0[i]);
-        mx = fmaxf(mx, cf0[i]);
-      }
-      if (v1) {
-        am1 = fmaxf(am1, fabsf(cf1[i]));
-        mn = fminf(mn, cf1[i]);
-        mx = fmaxf(mx, cf1[i]);
+    for (int i = 0; i < RM; i += 4) {
+      if (i < k) {
+        const float4 c4 = *reinterpret_cast<const float4*>(L.Ys + row * RM + i);
+        const float cv[4] = {c4.x, c4.y, c4.z, c4.w};
+#pragma unroll
+        for (int u = 0; u < 4; ++u)
+          if (i + u < k) {
+            am = fmaxf(am, fabsf(cv[u]));
+            mn = fminf(mn, cv[u]);
+            mx = fmaxf(mx, cv[u]);
+          }
       }
     }
+  };
+  if (v0) row_stats(t, am0);
+  if (v1) row_stats(t + kThreads, am1);
   // block reductions: absmax, min, max
   float* fred = (float*)L.red;
   __syncthreads();
@@ -1089,14 +1148,23 @@ __device__ __forceinline__ void run_matrix(const RsvdParams& p, const Job& j, in
     }
   };
 #pragma unroll
-  for (int i = 0; i < RM; ++i) {
+  for (int i = 0; i < RM; i += 4) {
     if (i < j.kp) {
-      int8_t q0 = 0, q1 = 0;
-      if (i < k) {
-        q0 = (int8_t)(int)rintf(cf0[i] / s0);  // IEEE division, ties to even
-        q1 = (int8_t)(int)rintf(cf1[i] / s1);
+      const float4 zero4 = make_float4(0.f, 0.f, 0.f, 0.f);
+      const float4 a4 = v0 ? *reinterpret_cast<const float4*>(L.Ys + t * RM + i) : zero4;
+      const float4 b4 = v1 ? *reinterpret_cast<const float4*>(L.Ys + (t + kThreads) * RM + i) : zero4;
+      const float ca[4] = {a4.x, a4.y, a4.z, a4.w}, cb[4] = {b4.x, b4.y, b4.z, b4.w};
+#pragma unroll
+      for (int u = 0; u < 4; ++u) {
+        if (i + u < j.kp) {
+          int8_t q0 = 0, q1 = 0;
+          if (i + u < k) {
+            q0 = (int8_t)(int)rintf(ca[u] / s0);  // IEEE division, ties to even
+            q1 = (int8_t)(int)rintf(cb[u] / s1);
+          }
+          put(i + u, q0, q1);
+        }
       }
-      put(i, q0, q1);
     }
   }
   for (int i = RM; i < j.kp; ++i) put(i, 0, 0);
