@@ -719,57 +719,66 @@ __device__ __forceinline__ void jacobi_rotation(double app, double aqq, double a
   sn = sd * f;
 }
 
-// Lane `src`'s double (src < 64, per lane), through the LDS crossbar; all
-// lanes must be active.
-__device__ __forceinline__ double lane_fetch(double v, int src) {
-  const long long u = __double_as_longlong(v);
-  const int lo = __builtin_amdgcn_ds_bpermute(src << 2, (int)(u & 0xffffffffLL));
-  const int hi = __builtin_amdgcn_ds_bpermute(src << 2, (int)(u >> 32));
-  return __longlong_as_double(((long long)hi << 32) | (unsigned)lo);
-}
-
-// Cyclic parallel Jacobi on the symmetric Gs by the whole workgroup:
-// Gs -> diagonal, Ws = eigenvectors.  The round-robin pairing runs over the
-// P = r rounded up to even players (P - 1 rounds per sweep); rows and
-// columns >= r are zeroed first, so a padded player's rotations are the
-// identity.  The matrix is double-buffered (Gs, G2), so a round is one
-// barrier-separated step.  In it every thread first issues all its reads
-// of the current buffer, then:
-//   * each wave computes the rotations (c, s) of all the round's pairs, lane
-//     l taking pair l % NP (every wave computes the same values from the
-//     same entries), and each lane fetches the rotations it needs from the
-//     lanes of its own wave (ds_bpermute: no LDS traffic, no barrier);
+// Cyclic parallel Jacobi on the symmetric r x r Gram in Gs (row-major,
+// stride RM) by the whole workgroup.  On return Gs[i][i] holds eigenvalue i
+// (the rest of Gs, and G2, are garbage) and Ws holds the eigenvectors
+// transposed: Ws[i * P + c] = W[c][i] (row i is eigenvector i), P = r
+// rounded up to even.
+//
+// Round-robin pairing over P players at fixed positions: in every round
+// pair m sits at positions (m, P - 1 - m); between rounds the player at
+// position x >= 1 moves to position x + 1 (P - 1 wraps to 1), so after the
+// P - 1 rounds of a sweep every player is back at its start and every pair
+// has met once.  The matrix is kept in position coordinates, upper triangle
+// only (element (x, y) at min * P + max), double-buffered (Gs, G2): a round
+// rotates the pairs in place of the positions and writes each element to
+// its moved position in the other buffer.  So every thread reads and writes
+// the same LDS offsets in every round, computed once; a round is one
+// barrier-separated step.  A padded player's row and column are zero, so
+// its rotations are the identity.  In a round every thread first issues its
+// reads, then:
+//   * each wave computes the rotations (c, s) of all pairs, lane l taking
+//     pair l % NP (every wave computes the same values from the same
+//     entries); lanes l < NP store them in the wave's own slot of rot and the
+//     wave's lanes read back those they need (no barrier);
 //   * thread i < NB rotates the 2x2 block (pair mi, pair mk), mi <= mk, from
-//     both sides (G <- J^T G J) into the other buffer, with its mirror;
-//   * thread t rotates rows t / NP, t / NP + cnt, ... of pair t % NP of Ws
-//     from the right, in place (cnt = number of threads with that pair).
-// The pairs of a round partition the players, so the blocks cover the
-// P x P matrix once.  Each thread walks the players of its pairs with
-// PairWalk counters.  Stops when the off-diagonal mass is <= 1e-10 of the
+//     both sides (G <- J^T G J) into the other buffer (a diagonal block has
+//     three distinct entries);
+//   * the (pair m, row c) items of the eigenvector update, m * P + c = t,
+//     t + kThreads, ..., rotate entries (players of m, c) of Ws in place;
+//     the players of a position move by one per round, so the two LDS
+//     offsets of an item are updated by one compare and select each.
+// Stops at a sweep boundary when the off-diagonal mass is <= 1e-10 of the
 // diagonal mass (the off-diagonal norm below 1e-5 of the diagonal's): the
 // eigenvectors then mix the retained and the dropped directions by ~1e-5,
 // which moves the reconstruction error of the truncated fit by ~1e-8
 // relative (second order), far below the fp32 and INT8 rounding of the
-// outputs.  On return the diagonal of Gs holds the eigenvalues (its other
-// entries, and G2, are garbage).
-// scratch: >= 2 * kThreads / 64 doubles.
+// outputs.
+// scratch: >= 2 * kThreads / 64 doubles; rot: >= kThreads / 64 * RM / 2
+// (c, s) pairs, 16-byte aligned.
 template <int RM>
-__device__ __forceinline__ void jacobi_eig(double* Gs, double* G2, double* Ws, double* scratch, int r) {
+__device__ __forceinline__ void jacobi_eig(double* Gs, double* G2, double* Ws, double* scratch, double2* rot, int r) {
   static_assert(RM % 2 == 0, "even player count");
   constexpr int NP = RM / 2;
   constexpr int NB = NP * (NP + 1) / 2;  // upper-triangular 2x2 blocks
   constexpr int NW = kThreads / 64;
-  constexpr int WR = (RM + kThreads / NP - 1) / (kThreads / NP);  // Ws rows per thread, at most
+  constexpr int WJ = (NP * RM + kThreads - 1) / kThreads;  // eigenvector items per thread, at most
   static_assert(NB <= kThreads && NP <= 64 && 2 * NW <= 128, "one block per thread; one pair per lane");
-  const int t = threadIdx.x, lane = t & 63;
+  const int t = threadIdx.x, lane = t & 63, w = t >> 6;
   const int P = r + (r & 1), NPr = P / 2, NBr = NPr * (NPr + 1) / 2;
   double* part = scratch;  // [NW][2] partial sums
-  for (int e = t; e < RM * RM; e += kThreads) {
-    const int i = e / RM, k = e % RM;
+  double2* wrot = rot + w * NP;
+  auto at = [P](int x, int y) __attribute__((always_inline)) { return min(x, y) * P + max(x, y); };
+  auto mv = [P](int x) __attribute__((always_inline)) { return x == 0 ? 0 : (x == P - 1 ? 1 : x + 1); };
+  for (int e = t; e < P * P; e += kThreads) {
+    const int i = e / P, k = e % P;
     Ws[e] = (i == k) ? 1.0 : 0.0;
-    if (i >= r || k >= r) Gs[e] = 0.0;
-    G2[e] = 0.0;
+    if (i <= k) G2[e] = (k < r) ? Gs[i * RM + k] : 0.0;
   }
+  // fixed offsets: the rotation entries of pair l % NP, the block's reads
+  // and its moved writes
+  const int mr = lane % NPr;
+  const int o_pp = at(mr, mr), o_qq = at(P - 1 - mr, P - 1 - mr), o_pq = at(mr, P - 1 - mr);
   const bool blk = t < NBr;
   int mi = 0, mk = 0;
   if (blk) {
@@ -778,107 +787,118 @@ __device__ __forceinline__ void jacobi_eig(double* Gs, double* G2, double* Ws, d
     if (mk * (mk + 1) / 2 > t) --mk;
     mi = t - mk * (mk + 1) / 2;
   }
-  const int mv = t % NPr, vcnt = (kThreads - mv + NPr - 1) / NPr, vrow = t / NPr;
-  const int mr = lane % NPr;
-  double* cur = Gs;
-  double* nxt = G2;
+  const int xi = mi, yi = P - 1 - mi, xk = mk, yk = P - 1 - mk;
+  const int r00 = at(xi, xk), r01 = at(xi, yk), r10 = at(yi, xk), r11 = at(yi, yk);
+  const int w00 = at(mv(xi), mv(xk)), w01 = at(mv(xi), mv(yk)), w10 = at(mv(yi), mv(xk)), w11 = at(mv(yi), mv(yk));
+  // eigenvector items (pair m, row c): LDS offsets of (player at position m, c)
+  // and (player at position P - 1 - m, c); player 0 never moves
+  const int nitem = NPr * P;
+  int im[WJ], op[WJ], oq[WJ];
+  bool iv[WJ];
+#pragma unroll
+  for (int jj = 0; jj < WJ; ++jj) {
+    const int e = t + jj * kThreads;
+    iv[jj] = e < nitem;
+    const int m = iv[jj] ? e / P : 0, c = iv[jj] ? e % P : 0;
+    im[jj] = m;
+    op[jj] = m * P + c;
+    oq[jj] = (P - 1 - m) * P + c;
+  }
+  double* cur = G2;
+  double* nxt = Gs;
+  auto round = [&](const double* gc, double* gn) __attribute__((always_inline)) {
+    const double app = gc[o_pp], aqq = gc[o_qq], apq = gc[o_pq];
+    double a00 = 0.0, a01 = 0.0, a10 = 0.0, a11 = 0.0;
+    if (blk) {
+      a00 = gc[r00];
+      a01 = gc[r01];
+      a10 = gc[r10];
+      a11 = gc[r11];
+    }
+    double vp[WJ], vq[WJ];
+#pragma unroll
+    for (int jj = 0; jj < WJ; ++jj) {
+      vp[jj] = vq[jj] = 0.0;
+      if (iv[jj]) {
+        vp[jj] = Ws[op[jj]];
+        vq[jj] = Ws[oq[jj]];
+      }
+    }
+    double c0, s0;
+    jacobi_rotation(app, aqq, apq, c0, s0);
+    if (lane < NPr) wrot[lane] = make_double2(c0, s0);
+    wave_sync();
+    if (blk) {
+      const double2 ri = wrot[mi], rk = wrot[mk];
+      const double ci = ri.x, si = ri.y, ck = rk.x, sk = rk.y;
+      const double b00 = ci * a00 - si * a10, b01 = ci * a01 - si * a11;  // rows: J^T A
+      const double b10 = si * a00 + ci * a10, b11 = si * a01 + ci * a11;
+      const double n00 = ck * b00 - sk * b01, n01 = sk * b00 + ck * b01;  // columns: (J^T A) J
+      const double n10 = ck * b10 - sk * b11, n11 = sk * b10 + ck * b11;
+      gn[w00] = n00;
+      gn[w01] = n01;
+      gn[w11] = n11;
+      if (mi != mk) gn[w10] = n10;  // a diagonal block's (y, x) is its (x, y)
+    }
+#pragma unroll
+    for (int jj = 0; jj < WJ; ++jj) {
+      if (iv[jj]) {
+        const double2 rm = wrot[im[jj]];
+        Ws[op[jj]] = rm.x * vp[jj] - rm.y * vq[jj];
+        Ws[oq[jj]] = rm.y * vp[jj] + rm.x * vq[jj];
+      }
+      // next round's players: p -> p - 1 (1 -> P - 1), player 0 fixed
+      if (im[jj] != 0) op[jj] = op[jj] < 2 * P ? op[jj] + (P - 2) * P : op[jj] - P;
+      oq[jj] = oq[jj] < 2 * P ? oq[jj] + (P - 2) * P : oq[jj] - P;
+    }
+    __syncthreads();
+  };
   __syncthreads();
   for (int sweep = 0; sweep < 30; ++sweep) {
     double off = 0.0, dia = 0.0;
-    for (int e = t; e < RM * RM; e += kThreads) {
+    for (int e = t; e < P * P; e += kThreads) {
+      const int i = e / P, k = e % P;
       const double v = cur[e];
-      if (e / RM == e % RM)
+      if (i == k)
         dia += v * v;
-      else
-        off += v * v;
+      else if (i < k)
+        off += 2.0 * (v * v);
     }
 #pragma unroll
     for (int o = 32; o > 0; o >>= 1) {
       off += __shfl_xor(off, o);
       dia += __shfl_xor(dia, o);
     }
-    if ((t & 63) == 0) {
-      part[2 * (t >> 6)] = off;
-      part[2 * (t >> 6) + 1] = dia;
+    if (lane == 0) {
+      part[2 * w] = off;
+      part[2 * w + 1] = dia;
     }
     __syncthreads();
     off = 0.0;
     dia = 0.0;
 #pragma unroll
-    for (int w = 0; w < NW; ++w) {  // same order in every thread: a uniform decision
-      off += part[2 * w];
-      dia += part[2 * w + 1];
+    for (int ww = 0; ww < NW; ++ww) {  // same order in every thread: a uniform decision
+      off += part[2 * ww];
+      dia += part[2 * ww + 1];
     }
     if (off <= 1e-10 * dia || dia == 0.0) break;
-    PairWalk wr, wi, wk, wv;
-    wr.start(P, mr);
-    wi.start(P, mi);
-    wk.start(P, mk);
-    wv.start(P, mv);
-    for (int step = 0; step < P - 1; ++step, wr.next(), wi.next(), wk.next(), wv.next()) {
-      // all reads of the current buffer first
-      int pr, qr, pi, qi, pk, qk, pm, qm;
-      wr.players(pr, qr);
-      wi.players(pi, qi);
-      wk.players(pk, qk);
-      wv.players(pm, qm);
-      const double app = cur[__umul24(pr, RM) + pr], aqq = cur[__umul24(qr, RM) + qr];
-      const double apq = cur[__umul24(pr, RM) + qr];
-      double a00 = 0.0, a01 = 0.0, a10 = 0.0, a11 = 0.0;
-      if (blk) {
-        a00 = cur[__umul24(pi, RM) + pk];
-        a01 = cur[__umul24(pi, RM) + qk];
-        a10 = cur[__umul24(qi, RM) + pk];
-        a11 = cur[__umul24(qi, RM) + qk];
-      }
-      double vp[WR], vq[WR];
-#pragma unroll
-      for (int jr = 0; jr < WR; ++jr) {
-        const int c = vrow + jr * vcnt;
-        vp[jr] = vq[jr] = 0.0;
-        if (c < P) {
-          vp[jr] = Ws[__umul24(c, RM) + pm];
-          vq[jr] = Ws[__umul24(c, RM) + qm];
-        }
-      }
-      double c0, s0;
-      jacobi_rotation(app, aqq, apq, c0, s0);
-      const double ci = lane_fetch(c0, mi), si = lane_fetch(s0, mi);
-      const double ck = lane_fetch(c0, mk), sk = lane_fetch(s0, mk);
-      const double cm = lane_fetch(c0, mv), sm = lane_fetch(s0, mv);
-      if (blk) {
-        const double b00 = ci * a00 - si * a10, b01 = ci * a01 - si * a11;  // rows: J^T A
-        const double b10 = si * a00 + ci * a10, b11 = si * a01 + ci * a11;
-        const double n00 = ck * b00 - sk * b01, n01 = sk * b00 + ck * b01;  // columns: (J^T A) J
-        const double n10 = ck * b10 - sk * b11, n11 = sk * b10 + ck * b11;
-        nxt[__umul24(pi, RM) + pk] = n00;
-        nxt[__umul24(pi, RM) + qk] = n01;
-        nxt[__umul24(qi, RM) + pk] = n10;
-        nxt[__umul24(qi, RM) + qk] = n11;
-        if (mi != mk) {
-          nxt[__umul24(pk, RM) + pi] = n00;
-          nxt[__umul24(qk, RM) + pi] = n01;
-          nxt[__umul24(pk, RM) + qi] = n10;
-          nxt[__umul24(qk, RM) + qi] = n11;
-        }
-      }
-#pragma unroll
-      for (int jr = 0; jr < WR; ++jr) {
-        const int c = vrow + jr * vcnt;
-        if (c < P) {
-          Ws[__umul24(c, RM) + pm] = cm * vp[jr] - sm * vq[jr];
-          Ws[__umul24(c, RM) + qm] = sm * vp[jr] + cm * vq[jr];
-        }
-      }
-      __syncthreads();
-      double* tmp = cur;
-      cur = nxt;
-      nxt = tmp;
+    double* A = cur;
+    double* B = nxt;
+    int step = 0;
+    for (; step + 1 < P - 1; step += 2) {
+      round(A, B);
+      round(B, A);
+    }
+    if (step < P - 1) {  // odd number of rounds: the sweep ends in the other buffer
+      round(A, B);
+      cur = B;
+      nxt = A;
     }
   }
-  if (cur != Gs) {  // uniform: every thread ran the same rounds
-    for (int e = t; e < RM; e += kThreads) Gs[e * RM + e] = cur[e * RM + e];
-  }
+  // eigenvalues to the diagonal of Gs (stride RM); cur may overlap Gs
+  const double ev = t < P ? cur[t * P + t] : 0.0;
+  __syncthreads();
+  if (t < P) Gs[t * RM + t] = ev;
   __syncthreads();
 }
 
@@ -887,6 +907,7 @@ __device__ __forceinline__ void run_matrix(const RsvdParams& p, const Job& j, in
                            const float* omega_in, long dbg_index) {
   const int t = threadIdx.x;
   const int r = j.r, k = j.k;
+  const int P = r + (r & 1);  // Jacobi players: the eigenvectors are rows of Ws with stride P
   // ---- sketch
   for (int e = t; e < 128 * RM; e += kThreads) L.Zs[e] = 0.f;
   __syncthreads();
@@ -958,7 +979,7 @@ __device__ __forceinline__ void run_matrix(const RsvdParams& p, const Job& j, in
   __syncthreads();
   gram_mfma<RM>(L.Zs, cols, r, L.Gs);  // Bp Bp^T
   __syncthreads();
-  jacobi_eig<RM>(L.Gs, L.G2, L.Ws, L.red, r);
+  jacobi_eig<RM>(L.Gs, L.G2, L.Ws, L.red, reinterpret_cast<double2*>(L.Wf), r);  // Wf: dead here
   // ---- eigenvalues in descending order: lane c takes rank = #{larger, or equal with lower index}
   if (t < r) {
     const double lc = L.Gs[t * RM + t];
@@ -976,7 +997,7 @@ __device__ __forceinline__ void run_matrix(const RsvdParams& p, const Job& j, in
     float v = 0.f;
     if (i < k) {
       const int oi = L.ord[i];
-      v = (float)(L.Ws[c * RM + oi] * sqrt(fmax(L.Gs[oi * RM + oi], 0.0)));
+      v = (float)(L.Ws[oi * P + c] * sqrt(fmax(L.Gs[oi * RM + oi], 0.0)));
     }
     L.Wf[e] = v;
   }
@@ -1056,8 +1077,8 @@ __device__ __forceinline__ void run_matrix(const RsvdParams& p, const Job& j, in
       double a0 = 0.0, a1 = 0.0;
 #pragma unroll
       for (int c = 0; c < RM; c += 2) {
-        if (c < r) a0 = fma(L.Ws[c * RM + oi], (double)z[c], a0);
-        if (c + 1 < r) a1 = fma(L.Ws[(c + 1) * RM + oi], (double)z[c + 1], a1);
+        if (c < r) a0 = fma(L.Ws[oi * P + c], (double)z[c], a0);
+        if (c + 1 < r) a1 = fma(L.Ws[oi * P + c + 1], (double)z[c + 1], a1);
       }
       L.Zs[i * cols + d] = (float)(a0 + a1);
     }
