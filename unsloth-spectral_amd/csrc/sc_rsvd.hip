@@ -575,10 +575,13 @@ __device__ __forceinline__ void cholesky_inv_wave(const double* Gs, float* Xf, i
           row[jc] = dead ? 0.0 : piv * il;                // L[jc][jc] = sqrt(piv)
           il_own = il;
         }
+        // the trailing update with the multiplier zeroed on lanes <= jc, so
+        // the FMAs need no per-element select
+        const double lm = lane > jc ? -row[jc] : 0.0;
 #pragma unroll
         for (int k = jc + 1; k < RM; ++k) {
           const double lk = lane_bcast(row[jc], k);       // L[k][jc]
-          if (lane > jc) row[k] = fma(-row[jc], lk, row[k]);
+          row[k] = fma(lm, lk, row[k]);
         }
       }
     }
@@ -592,11 +595,11 @@ __device__ __forceinline__ void cholesky_inv_wave(const double* Gs, float* Xf, i
 #pragma unroll
         for (int n = 0; n <= m; ++n) y[n] = ((n == m ? 1.0 : 0.0) - y[n]) * il_own;
       }
-      const double lim = row[m];  // L[lane][m]
+      const double lim = lane > m ? row[m] : 0.0;  // L[lane][m]; 0 leaves the finished rows unchanged
 #pragma unroll
       for (int n = 0; n <= m; ++n) {
         const double ymn = lane_bcast(y[n], m);
-        if (lane > m) y[n] = fma(lim, ymn, y[n]);
+        y[n] = fma(lim, ymn, y[n]);
       }
     }
     // X[n][lane] = Y[lane][n]
@@ -636,8 +639,12 @@ __device__ __forceinline__ void normalize_cols(float* Ys, int rows, int r, float
 // Rows of Ys <- rows of Ys X (X upper triangular, fp32 in Xf).  Thread t
 // takes rows t and t + kThreads together (kept in registers), so each
 // float4 of X read from LDS (a broadcast) serves both.  Output columns go
-// four at a time in a runtime loop, which bounds the loads in flight; no
-// dependency chain across columns.
+// four at a time.  For RM = 40 (one workgroup per CU: registers to spare)
+// the column groups are unrolled, so the triangle (X[m][c] = 0 for m > c)
+// is skipped at compile time with no branches, and a scheduling barrier
+// after each group bounds the loads in flight; for RM = 24 (two workgroups
+// per CU: at most 256 VGPRs) they run in a loop that skips the triangle
+// with a uniform test per row.  No dependency chain across columns.
 template <int RM>
 __device__ __forceinline__ void apply_rinv(float* Ys, int rows, const float* Xf) {
   static_assert(RM % 4 == 0 && kMaxRows <= 2 * kThreads, "two rows per thread, float4 columns");
@@ -651,25 +658,50 @@ __device__ __forceinline__ void apply_rinv(float* Ys, int rows, const float* Xf)
     ya[c] = a4.x; ya[c + 1] = a4.y; ya[c + 2] = a4.z; ya[c + 3] = a4.w;
     yb[c] = b4.x; yb[c + 1] = b4.y; yb[c + 2] = b4.z; yb[c + 3] = b4.w;
   }
-#pragma unroll 1
-  for (int c = 0; c < RM; c += 4) {
-    float4 qa = make_float4(0.f, 0.f, 0.f, 0.f), qb = qa;
+  auto group = [&](int c, int m) __attribute__((always_inline)) {  // row m's share of columns c..c+3
+    const float4 x4 = *reinterpret_cast<const float4*>(Xf + m * RM + c);
+    float4 d;
+    d.x = x4.x;
+    d.y = x4.y;
+    d.z = x4.z;
+    d.w = x4.w;
+    return d;
+  };
+  auto fma4 = [](float4& q, float y, const float4& x) __attribute__((always_inline)) {
+    q.x = fmaf(y, x.x, q.x);
+    q.y = fmaf(y, x.y, q.y);
+    q.z = fmaf(y, x.z, q.z);
+    q.w = fmaf(y, x.w, q.w);
+  };
+  if constexpr (RM > 24) {
 #pragma unroll
-    for (int m = 0; m < RM; ++m) {
-      if (m < c + 4) {  // X[m][c..c+3] = 0 below the diagonal
-        const float4 x4 = *reinterpret_cast<const float4*>(Xf + m * RM + c);
-        qa.x = fmaf(ya[m], x4.x, qa.x);
-        qa.y = fmaf(ya[m], x4.y, qa.y);
-        qa.z = fmaf(ya[m], x4.z, qa.z);
-        qa.w = fmaf(ya[m], x4.w, qa.w);
-        qb.x = fmaf(yb[m], x4.x, qb.x);
-        qb.y = fmaf(yb[m], x4.y, qb.y);
-        qb.z = fmaf(yb[m], x4.z, qb.z);
-        qb.w = fmaf(yb[m], x4.w, qb.w);
+    for (int c = 0; c < RM; c += 4) {
+      float4 qa = make_float4(0.f, 0.f, 0.f, 0.f), qb = qa;
+#pragma unroll
+      for (int m = 0; m < c + 4; ++m) {  // X[m][c..c+3] = 0 for m >= c + 4
+        const float4 x4 = group(c, m);
+        fma4(qa, ya[m], x4);
+        fma4(qb, yb[m], x4);
       }
+      if (va) *reinterpret_cast<float4*>(Ys + t * RM + c) = qa;
+      if (vb) *reinterpret_cast<float4*>(Ys + (t + kThreads) * RM + c) = qb;
+      __builtin_amdgcn_sched_barrier(0);
     }
-    if (va) *reinterpret_cast<float4*>(Ys + t * RM + c) = qa;
-    if (vb) *reinterpret_cast<float4*>(Ys + (t + kThreads) * RM + c) = qb;
+  } else {
+#pragma unroll 1
+    for (int c = 0; c < RM; c += 4) {
+      float4 qa = make_float4(0.f, 0.f, 0.f, 0.f), qb = qa;
+#pragma unroll
+      for (int m = 0; m < RM; ++m) {
+        if (m < c + 4) {  // X[m][c..c+3] = 0 below the diagonal
+          const float4 x4 = group(c, m);
+          fma4(qa, ya[m], x4);
+          fma4(qb, yb[m], x4);
+        }
+      }
+      if (va) *reinterpret_cast<float4*>(Ys + t * RM + c) = qa;
+      if (vb) *reinterpret_cast<float4*>(Ys + (t + kThreads) * RM + c) = qb;
+    }
   }
 }
 
@@ -723,7 +755,7 @@ __device__ __forceinline__ void jacobi_rotation(double app, double aqq, double a
 // stride RM) by the whole workgroup.  On return Gs[i][i] holds eigenvalue i
 // (the rest of Gs, and G2, are garbage) and Ws holds the eigenvectors
 // transposed: Ws[i * P + c] = W[c][i] (row i is eigenvector i), P = r
-// rounded up to even.
+// rounded up to even; Ws beyond its P x P entries is zero.
 //
 // Round-robin pairing over P players at fixed positions: in every round
 // pair m sits at positions (m, P - 1 - m); between rounds the player at
@@ -770,10 +802,10 @@ __device__ __forceinline__ void jacobi_eig(double* Gs, double* G2, double* Ws, d
   double2* wrot = rot + w * NP;
   auto at = [P](int x, int y) __attribute__((always_inline)) { return min(x, y) * P + max(x, y); };
   auto mv = [P](int x) __attribute__((always_inline)) { return x == 0 ? 0 : (x == P - 1 ? 1 : x + 1); };
-  for (int e = t; e < P * P; e += kThreads) {
+  for (int e = t; e < RM * RM; e += kThreads) {  // all of Ws: its readers take whole rows of RM entries
     const int i = e / P, k = e % P;
-    Ws[e] = (i == k) ? 1.0 : 0.0;
-    if (i <= k) G2[e] = (k < r) ? Gs[i * RM + k] : 0.0;
+    Ws[e] = (e < P * P && i == k) ? 1.0 : 0.0;
+    if (e < P * P && i <= k) G2[e] = (k < r) ? Gs[i * RM + k] : 0.0;
   }
   // fixed offsets: the rotation entries of pair l % NP, the block's reads
   // and its moved writes
@@ -1017,7 +1049,7 @@ __device__ __forceinline__ void run_matrix(const RsvdParams& p, const Job& j, in
       const float q0 = v0 ? L.Ys[t * RM + c] : 0.f, q1 = v1 ? L.Ys[(t + kThreads) * RM + c] : 0.f;
 #pragma unroll
       for (int i = 0; i < RM; i += 4) {
-        if (i < k) {
+        {  // all RM columns: Wf[c][i] = 0 for i >= k, so those accumulators stay 0 (no branches)
           const float4 w = *reinterpret_cast<const float4*>(L.Wf + c * RM + i);
           cf0[i] = fmaf(q0, w.x, cf0[i]);
           cf0[i + 1] = fmaf(q0, w.y, cf0[i + 1]);
@@ -1073,12 +1105,15 @@ __device__ __forceinline__ void run_matrix(const RsvdParams& p, const Job& j, in
     __syncthreads();  // every Bp^T row is in registers
 #pragma unroll 2
     for (int i = t / cols; i < k; i += istep) {
-      const int oi = L.ord[i];
+      // whole rows of RM entries, no branches: z[c] = 0 for c >= r (the
+      // columns of Q beyond r are zero) and Ws is zero beyond P x P
+      const double* wr = L.Ws + L.ord[i] * P;
       double a0 = 0.0, a1 = 0.0;
 #pragma unroll
       for (int c = 0; c < RM; c += 2) {
-        if (c < r) a0 = fma(L.Ws[oi * P + c], (double)z[c], a0);
-        if (c + 1 < r) a1 = fma(L.Ws[oi * P + c + 1], (double)z[c + 1], a1);
+        const double2 w2 = *reinterpret_cast<const double2*>(wr + c);
+        a0 = fma(w2.x, (double)z[c], a0);
+        a1 = fma(w2.y, (double)z[c + 1], a1);
       }
       L.Zs[i * cols + d] = (float)(a0 + a1);
     }
@@ -1116,17 +1151,15 @@ __device__ __forceinline__ void run_matrix(const RsvdParams& p, const Job& j, in
   float am0 = 0.f, am1 = 0.f, mn = INFINITY, mx = -INFINITY;
   auto row_stats = [&](int row, float& am) __attribute__((always_inline)) {
 #pragma unroll
-    for (int i = 0; i < RM; i += 4) {
-      if (i < k) {
-        const float4 c4 = *reinterpret_cast<const float4*>(L.Ys + row * RM + i);
-        const float cv[4] = {c4.x, c4.y, c4.z, c4.w};
+    for (int i = 0; i < RM; i += 4) {  // columns >= k hold 0: masked by selects, no branches
+      const float4 c4 = *reinterpret_cast<const float4*>(L.Ys + row * RM + i);
+      const float cv[4] = {c4.x, c4.y, c4.z, c4.w};
 #pragma unroll
-        for (int u = 0; u < 4; ++u)
-          if (i + u < k) {
-            am = fmaxf(am, fabsf(cv[u]));
-            mn = fminf(mn, cv[u]);
-            mx = fmaxf(mx, cv[u]);
-          }
+      for (int u = 0; u < 4; ++u) {
+        const bool in = i + u < k;
+        am = fmaxf(am, fabsf(cv[u]));
+        mn = fminf(mn, in ? cv[u] : INFINITY);
+        mx = fmaxf(mx, in ? cv[u] : -INFINITY);
       }
     }
   };
