@@ -377,7 +377,8 @@ __device__ __forceinline__ void gemm_cols_mfma(const Job& j, int rows, int cols,
       half8_t bh, bl;
 #pragma unroll
       for (int e = 0; e < 8; ++e) {
-        const float v = c < RM ? Ys[(k0 + 8 * g + e) * RM + c] : 0.f;
+        const float yv = Ys[(k0 + 8 * g + e) * RM + min(c, RM - 1)];  // in bounds: no exec branch
+        const float v = c < RM ? yv : 0.f;
         h16 hi, lo;
         split16(v, hi, lo);
         bh[e] = hi;
@@ -429,8 +430,9 @@ __device__ __forceinline__ void gram_mfma(const float* S, int nrows, int r, doub
         double av[4], bv[4];
 #pragma unroll
         for (int u = 0; u < 4; ++u) {
-          av[u] = ca < RM ? (double)S[(k0 + 4 * u + g) * RM + ca] : 0.0;
-          bv[u] = cb < RM ? (double)S[(k0 + 4 * u + g) * RM + cb] : 0.0;
+          const float sa = S[(k0 + 4 * u + g) * RM + min(ca, RM - 1)], sb = S[(k0 + 4 * u + g) * RM + min(cb, RM - 1)];
+          av[u] = ca < RM ? (double)sa : 0.0;
+          bv[u] = cb < RM ? (double)sb : 0.0;
         }
         acc = __builtin_amdgcn_mfma_f64_16x16x4f64(av[0], bv[0], acc, 0, 0, 0);
         acc1 = __builtin_amdgcn_mfma_f64_16x16x4f64(av[1], bv[1], acc1, 0, 0, 0);
@@ -475,7 +477,7 @@ __device__ __forceinline__ void gram_rows_mfma(const float* S, int nrows, int r,
     for (int u = 0; u < 2; ++u)
 #pragma unroll
       for (int ct = 0; ct < CT; ++ct)
-        v[u][ct] = 16 * ct + n < RM ? (double)S[(k0 + 4 * u + g) * RM + 16 * ct + n] : 0.0;
+        v[u][ct] = 16 * ct + n < RM ? (double)S[(k0 + 4 * u + g) * RM + min(16 * ct + n, RM - 1)] : 0.0;
 #pragma unroll
     for (int u = 0; u < 2; ++u) {
       int ti = 0;
