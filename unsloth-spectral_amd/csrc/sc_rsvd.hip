@@ -263,6 +263,25 @@ __device__ __forceinline__ void split16(float v, h16& hi, h16& lo) {
   lo = (h16)(v - (float)hi);
 }
 
+// split16 of eight values, converted in pairs (packed fp32 -> fp16
+// conversions; the subtraction stays scalar fp32).
+typedef float f32x2_t __attribute__((ext_vector_type(2)));
+typedef _Float16 f16x2_t __attribute__((ext_vector_type(2)));
+__device__ __forceinline__ void split16x8(const float (&v)[8], half8_t& hi, half8_t& lo) {
+#pragma unroll
+  for (int e = 0; e < 8; e += 2) {
+    const f32x2_t x = {v[e], v[e + 1]};
+    const f16x2_t h = __builtin_convertvector(x, f16x2_t);
+    const f32x2_t hb = __builtin_convertvector(h, f32x2_t);
+    const f32x2_t r = {x.x - hb.x, x.y - hb.y};
+    const f16x2_t l = __builtin_convertvector(r, f16x2_t);
+    hi[e] = h.x;
+    hi[e + 1] = h.y;
+    lo[e] = l.x;
+    lo[e + 1] = l.y;
+  }
+}
+
 // Ys[rows][RM] = M[rows][cols] Zs[cols][RM]; wave w takes row tiles w, w+4, ...
 template <int RM>
 __device__ __forceinline__ void gemm_rows_mfma(const Job& j, int rows, int cols, const float* Zs, float* Ys) {
@@ -375,15 +394,13 @@ __device__ __forceinline__ void gemm_cols_mfma(const Job& j, int rows, int cols,
     for (int ct = 0; ct < CT; ++ct) {
       const int c = 16 * ct + n;
       half8_t bh, bl;
+      float yv[8];
 #pragma unroll
       for (int e = 0; e < 8; ++e) {
-        const float yv = Ys[(k0 + 8 * g + e) * RM + min(c, RM - 1)];  // in bounds: no exec branch
-        const float v = c < RM ? yv : 0.f;
-        h16 hi, lo;
-        split16(v, hi, lo);
-        bh[e] = hi;
-        bl[e] = lo;
+        const float y = Ys[(k0 + 8 * g + e) * RM + min(c, RM - 1)];  // in bounds: no exec branch
+        yv[e] = c < RM ? y : 0.f;
       }
+      split16x8(yv, bh, bl);
 #pragma unroll
       for (int dt = 0; dt < 2; ++dt)
         if (dt < DT) {
@@ -407,6 +424,73 @@ __device__ __forceinline__ void gemm_cols_mfma(const Job& j, int rows, int cols,
 #pragma unroll
           for (int jj = 0; jj < 4; ++jj) Zs[((w * DT + dt) * 16 + 4 * g + jj) * RM + c] = acc[dt][ct][jj];
       }
+}
+
+// gemm_cols_mfma for two 16-column tiles of Ys (RM <= 32) and 128 columns
+// of M: wave w takes column tile w & 1 of Ys and the four d tiles
+// 4 (w >> 1) .. + 3, so each wave splits one column tile of Ys into fp16
+// hi + lo per staged tile instead of both.  Staging as gemm_cols_mfma.
+template <int RM>
+__device__ __forceinline__ void gemm_cols_mfma_ct(const Job& j, int rows, const float* Ys, float* Zs, h16* stage) {
+  static_assert((RM + 15) / 16 == 2, "two column tiles of Ys");
+  constexpr int cols = 128, pitch = cols + 8, cpr = cols / 8;
+  static_assert(kColTile * cpr == 2 * kThreads, "two 16-byte chunks per thread and tile");
+  const int t = threadIdx.x, lane = t & 63, g = lane >> 4, n = lane & 15, w = t >> 6;
+  const int ct = w & 1, dt0 = 4 * (w >> 1);
+  const int c = 16 * ct + n;
+  float4_t acc[4];
+#pragma unroll
+  for (int dt = 0; dt < 4; ++dt) acc[dt] = (float4_t)0.f;
+  const int c0 = t, c1 = t + kThreads;
+  uint4 nx0, nx1;
+  auto fetch = [&](int k0) __attribute__((always_inline)) {
+    nx0 = *reinterpret_cast<const uint4*>(row_ptr(j, k0 + c0 / cpr, cols) + (c0 % cpr) * 16);
+    nx1 = *reinterpret_cast<const uint4*>(row_ptr(j, k0 + c1 / cpr, cols) + (c1 % cpr) * 16);
+  };
+  auto put = [&]() __attribute__((always_inline)) {
+    *reinterpret_cast<uint4*>(stage + (c0 / cpr) * pitch + (c0 % cpr) * 8) = nx0;
+    *reinterpret_cast<uint4*>(stage + (c1 / cpr) * pitch + (c1 % cpr) * 8) = nx1;
+  };
+  fetch(0);
+  put();
+  __syncthreads();
+  for (int k0 = 0; k0 < rows; k0 += kColTile) {
+    const bool more = k0 + kColTile < rows;
+    if (more) fetch(k0 + kColTile);
+    half8_t a[4];
+#pragma unroll
+    for (int dt = 0; dt < 4; ++dt) {
+      const h16* p0 = stage + (8 * g + (n >> 2)) * pitch + (dt0 + dt) * 16 + 4 * (n & 3);
+      typedef __attribute__((address_space(3))) short4_t lds_s4;
+      const short4_t lo = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_s4*)(p0));
+      const short4_t hi = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_s4*)(p0 + 4 * pitch));
+      const half4_t l4 = __builtin_bit_cast(half4_t, lo), h4 = __builtin_bit_cast(half4_t, hi);
+      a[dt] = (half8_t){l4.x, l4.y, l4.z, l4.w, h4.x, h4.y, h4.z, h4.w};
+    }
+    float yv[8];
+#pragma unroll
+    for (int e = 0; e < 8; ++e) {
+      const float y = Ys[(k0 + 8 * g + e) * RM + min(c, RM - 1)];  // in bounds: no exec branch
+      yv[e] = c < RM ? y : 0.f;
+    }
+    half8_t bh, bl;
+    split16x8(yv, bh, bl);
+#pragma unroll
+    for (int dt = 0; dt < 4; ++dt) {
+      acc[dt] = __builtin_amdgcn_mfma_f32_16x16x32_f16(a[dt], bh, acc[dt], 0, 0, 0);
+      acc[dt] = __builtin_amdgcn_mfma_f32_16x16x32_f16(a[dt], bl, acc[dt], 0, 0, 0);
+    }
+    __syncthreads();  // every wave is done with this tile
+    if (more) {
+      put();
+      __syncthreads();
+    }
+  }
+  if (c < RM)
+#pragma unroll
+    for (int dt = 0; dt < 4; ++dt)
+#pragma unroll
+      for (int jj = 0; jj < 4; ++jj) Zs[((dt0 + dt) * 16 + 4 * g + jj) * RM + c] = acc[dt][jj];
 }
 
 // Gs[c1][c2] = sum_row S[row][c1] S[row][c2] (c1, c2 < r) in fp64 on MFMA
@@ -970,9 +1054,11 @@ __device__ __forceinline__ void run_matrix(const RsvdParams& p, const Job& j, in
     }
   };
   auto mul_mt = [&]() __attribute__((always_inline)) {  // Zs = M^T Ys
-    if (mf)
+    if (mf && (RM + 15) / 16 == 2 && cols == 128) {
+      if constexpr ((RM + 15) / 16 == 2) gemm_cols_mfma_ct<RM>(j, rows, L.Ys, L.Zs, reinterpret_cast<h16*>(L.Gs));
+    } else if (mf) {
       gemm_cols_mfma<RM>(j, rows, cols, L.Ys, L.Zs, reinterpret_cast<h16*>(L.Gs));
-    else
+    } else
       gemm_cols<RM>(j, rows, cols, L.Ys, L.Zs);
   };
   auto orth_ys = [&](int passes) __attribute__((always_inline)) {  // Ys <- Q of Ys (CholeskyQR passes)
@@ -1244,7 +1330,7 @@ __device__ __forceinline__ void run_matrix(const RsvdParams& p, const Job& j, in
 }
 
 template <int RM>
-__global__ __launch_bounds__(kThreads) void rsvd_generic_kernel(RsvdParams p) {
+__global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(RM <= 24 ? 2 : 1))) void rsvd_generic_kernel(RsvdParams p) {
   extern __shared__ __align__(16) char smem[];
   Lds<RM> L = carve<RM>(smem);
   const long i = blockIdx.x;
@@ -1293,7 +1379,7 @@ __device__ __forceinline__ int tier_new_blocks(const RsvdParams& p, const int32_
 }
 
 template <int RM>
-__global__ __launch_bounds__(kThreads) void rsvd_tier_kernel(RsvdParams p) {
+__global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(RM <= 24 ? 2 : 1))) void rsvd_tier_kernel(RsvdParams p) {
   extern __shared__ __align__(16) char smem[];
   const int u = blockIdx.x;
   const int kind = u & 1;
