@@ -426,21 +426,26 @@ __device__ __forceinline__ void gemm_cols_mfma(const Job& j, int rows, int cols,
       }
 }
 
-// gemm_cols_mfma for two 16-column tiles of Ys (RM <= 32) and 128 columns
-// of M: wave w takes column tile w & 1 of Ys and the four d tiles
-// 4 (w >> 1) .. + 3, so each wave splits one column tile of Ys into fp16
-// hi + lo per staged tile instead of both.  Staging as gemm_cols_mfma.
+// gemm_cols_mfma for 128 columns of M with each wave on one column tile
+// of Ys, so a wave splits one column tile into fp16 hi + lo per staged tile
+// instead of all of them: two tiles (RM <= 32): wave w takes tile w & 1 and
+// the four d tiles 4 (w >> 1) .. + 3; three tiles (RM <= 48): wave w < 3
+// takes tile w and all eight d tiles, wave 3 only stages.  Staging as
+// gemm_cols_mfma.
 template <int RM>
 __device__ __forceinline__ void gemm_cols_mfma_ct(const Job& j, int rows, const float* Ys, float* Zs, h16* stage) {
-  static_assert((RM + 15) / 16 == 2, "two column tiles of Ys");
+  constexpr int CT = (RM + 15) / 16;
+  static_assert(CT == 2 || CT == 3, "two or three column tiles of Ys");
+  constexpr int NDT = CT == 2 ? 4 : 8;  // d tiles per wave
   constexpr int cols = 128, pitch = cols + 8, cpr = cols / 8;
   static_assert(kColTile * cpr == 2 * kThreads, "two 16-byte chunks per thread and tile");
   const int t = threadIdx.x, lane = t & 63, g = lane >> 4, n = lane & 15, w = t >> 6;
-  const int ct = w & 1, dt0 = 4 * (w >> 1);
+  const int ct = CT == 2 ? (w & 1) : w, dt0 = CT == 2 ? 4 * (w >> 1) : 0;
+  const bool busy = ct < CT;  // wave-uniform
   const int c = 16 * ct + n;
-  float4_t acc[4];
+  float4_t acc[NDT];
 #pragma unroll
-  for (int dt = 0; dt < 4; ++dt) acc[dt] = (float4_t)0.f;
+  for (int dt = 0; dt < NDT; ++dt) acc[dt] = (float4_t)0.f;
   const int c0 = t, c1 = t + kThreads;
   uint4 nx0, nx1;
   auto fetch = [&](int k0) __attribute__((always_inline)) {
@@ -457,9 +462,10 @@ __device__ __forceinline__ void gemm_cols_mfma_ct(const Job& j, int rows, const 
   for (int k0 = 0; k0 < rows; k0 += kColTile) {
     const bool more = k0 + kColTile < rows;
     if (more) fetch(k0 + kColTile);
-    half8_t a[4];
+    if (busy) {
+    half8_t a[NDT];
 #pragma unroll
-    for (int dt = 0; dt < 4; ++dt) {
+    for (int dt = 0; dt < NDT; ++dt) {
       const h16* p0 = stage + (8 * g + (n >> 2)) * pitch + (dt0 + dt) * 16 + 4 * (n & 3);
       typedef __attribute__((address_space(3))) short4_t lds_s4;
       const short4_t lo = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_s4*)(p0));
@@ -476,9 +482,10 @@ __device__ __forceinline__ void gemm_cols_mfma_ct(const Job& j, int rows, const 
     half8_t bh, bl;
     split16x8(yv, bh, bl);
 #pragma unroll
-    for (int dt = 0; dt < 4; ++dt) {
+    for (int dt = 0; dt < NDT; ++dt) {
       acc[dt] = __builtin_amdgcn_mfma_f32_16x16x32_f16(a[dt], bh, acc[dt], 0, 0, 0);
       acc[dt] = __builtin_amdgcn_mfma_f32_16x16x32_f16(a[dt], bl, acc[dt], 0, 0, 0);
+    }
     }
     __syncthreads();  // every wave is done with this tile
     if (more) {
@@ -486,9 +493,9 @@ __device__ __forceinline__ void gemm_cols_mfma_ct(const Job& j, int rows, const 
       __syncthreads();
     }
   }
-  if (c < RM)
+  if (busy && c < RM)
 #pragma unroll
-    for (int dt = 0; dt < 4; ++dt)
+    for (int dt = 0; dt < NDT; ++dt)
 #pragma unroll
       for (int jj = 0; jj < 4; ++jj) Zs[((dt0 + dt) * 16 + 4 * g + jj) * RM + c] = acc[dt][jj];
 }
@@ -1054,8 +1061,8 @@ __device__ __forceinline__ void run_matrix(const RsvdParams& p, const Job& j, in
     }
   };
   auto mul_mt = [&]() __attribute__((always_inline)) {  // Zs = M^T Ys
-    if (mf && (RM + 15) / 16 == 2 && cols == 128) {
-      if constexpr ((RM + 15) / 16 == 2) gemm_cols_mfma_ct<RM>(j, rows, L.Ys, L.Zs, reinterpret_cast<h16*>(L.Gs));
+    if (mf && cols == 128) {
+      gemm_cols_mfma_ct<RM>(j, rows, L.Ys, L.Zs, reinterpret_cast<h16*>(L.Gs));
     } else if (mf) {
       gemm_cols_mfma<RM>(j, rows, cols, L.Ys, L.Zs, reinterpret_cast<h16*>(L.Gs));
     } else
