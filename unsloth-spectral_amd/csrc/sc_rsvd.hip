@@ -732,12 +732,9 @@ __device__ __forceinline__ void normalize_cols(float* Ys, int rows, int r, float
 // Rows of Ys <- rows of Ys X (X upper triangular, fp32 in Xf).  Thread t
 // takes rows t and t + kThreads together (kept in registers), so each
 // float4 of X read from LDS (a broadcast) serves both.  Output columns go
-// four at a time.  For RM = 40 (one workgroup per CU: registers to spare)
-// the column groups are unrolled, so the triangle (X[m][c] = 0 for m > c)
-// is skipped at compile time with no branches, and a scheduling barrier
-// after each group bounds the loads in flight; for RM = 24 (two workgroups
-// per CU: at most 256 VGPRs) they run in a loop that skips the triangle
-// with a uniform test per row.  No dependency chain across columns.
+// four at a time, unrolled, so the triangle (X[m][c] = 0 for m > c) is
+// skipped at compile time with no branches; a scheduling barrier after each
+// group bounds the loads in flight.  No dependency chain across columns.
 template <int RM>
 __device__ __forceinline__ void apply_rinv(float* Ys, int rows, const float* Xf) {
   static_assert(RM % 4 == 0 && kMaxRows <= 2 * kThreads, "two rows per thread, float4 columns");
@@ -766,35 +763,18 @@ __device__ __forceinline__ void apply_rinv(float* Ys, int rows, const float* Xf)
     q.z = fmaf(y, x.z, q.z);
     q.w = fmaf(y, x.w, q.w);
   };
-  if constexpr (RM > 24) {
 #pragma unroll
-    for (int c = 0; c < RM; c += 4) {
-      float4 qa = make_float4(0.f, 0.f, 0.f, 0.f), qb = qa;
+  for (int c = 0; c < RM; c += 4) {
+    float4 qa = make_float4(0.f, 0.f, 0.f, 0.f), qb = qa;
 #pragma unroll
-      for (int m = 0; m < c + 4; ++m) {  // X[m][c..c+3] = 0 for m >= c + 4
-        const float4 x4 = group(c, m);
-        fma4(qa, ya[m], x4);
-        fma4(qb, yb[m], x4);
-      }
-      if (va) *reinterpret_cast<float4*>(Ys + t * RM + c) = qa;
-      if (vb) *reinterpret_cast<float4*>(Ys + (t + kThreads) * RM + c) = qb;
-      __builtin_amdgcn_sched_barrier(0);
+    for (int m = 0; m < c + 4; ++m) {  // X[m][c..c+3] = 0 for m >= c + 4
+      const float4 x4 = group(c, m);
+      fma4(qa, ya[m], x4);
+      fma4(qb, yb[m], x4);
     }
-  } else {
-#pragma unroll 1
-    for (int c = 0; c < RM; c += 4) {
-      float4 qa = make_float4(0.f, 0.f, 0.f, 0.f), qb = qa;
-#pragma unroll
-      for (int m = 0; m < RM; ++m) {
-        if (m < c + 4) {  // X[m][c..c+3] = 0 below the diagonal
-          const float4 x4 = group(c, m);
-          fma4(qa, ya[m], x4);
-          fma4(qb, yb[m], x4);
-        }
-      }
-      if (va) *reinterpret_cast<float4*>(Ys + t * RM + c) = qa;
-      if (vb) *reinterpret_cast<float4*>(Ys + (t + kThreads) * RM + c) = qb;
-    }
+    if (va) *reinterpret_cast<float4*>(Ys + t * RM + c) = qa;
+    if (vb) *reinterpret_cast<float4*>(Ys + (t + kThreads) * RM + c) = qb;
+    __builtin_amdgcn_sched_barrier(0);
   }
 }
 
