@@ -142,25 +142,35 @@ template <int RM>
 struct Lds {
   float* Ys;     // [kMaxRows][RM]  Y / Q rows, later the coefficient rows
   float* Zs;     // [128][RM]       Z / Bp^T, later Vh [RM][cols]
-  double* Gs;    // [RM][RM]
-  double* G2;    // [RM][RM]        second buffer of the Jacobi iteration
-  double* Ws;    // [RM][RM]        eigenvectors
+  double* Gs;    // [RM][RM] + spare<RM>()
+  double* G2;    // [RM][RM] + spare<RM>()  second buffer of the Jacobi iteration
+  double* Ws;    // [RM][RM] + spare<RM>()  eigenvectors
   float* Wf;     // [RM][RM]        W[:, ord] * S for the coefficient product
   double* red;   // [128]
   int* ord;      // [RM]
   int* flag;     // [RM + 4]
 };
 
+// Spare doubles after each of Gs, G2 and Ws at RM = 40: per-lane sinks of
+// the Jacobi rounds' unused stores (so that every store is unconditional).
+// None at RM = 24, whose rounds mask the unused lanes instead: there the
+// spares would push the later arrays past the 64 KB reach of an LDS
+// instruction's immediate offset.
+template <int RM>
+constexpr int spare() {
+  return RM > 24 ? 64 : 0;
+}
+
 template <int RM>
 __device__ Lds<RM> carve(void* base) {
   Lds<RM> l;
   char* p = (char*)base;
   l.Gs = (double*)p;
-  p += sizeof(double) * RM * RM;
+  p += sizeof(double) * (RM * RM + spare<RM>());
   l.G2 = (double*)p;
-  p += sizeof(double) * RM * RM;
+  p += sizeof(double) * (RM * RM + spare<RM>());
   l.Ws = (double*)p;
-  p += sizeof(double) * RM * RM;
+  p += sizeof(double) * (RM * RM + spare<RM>());
   l.red = (double*)p;
   p += sizeof(double) * 128;
   l.Ys = (float*)p;
@@ -177,7 +187,7 @@ __device__ Lds<RM> carve(void* base) {
 
 template <int RM>
 constexpr size_t lds_bytes() {
-  return sizeof(double) * (3 * RM * RM + 128) + sizeof(float) * (kMaxRows * RM + 128 * RM + RM * RM) +
+  return sizeof(double) * (3 * (RM * RM + spare<RM>()) + 128) + sizeof(float) * (kMaxRows * RM + 128 * RM + RM * RM) +
          sizeof(int) * (2 * RM + 4);
 }
 
@@ -869,6 +879,10 @@ __device__ __forceinline__ void jacobi_eig(double* Gs, double* G2, double* Ws, d
   constexpr int NW = kThreads / 64;
   constexpr int WJ = (NP * RM + kThreads - 1) / kThreads;  // eigenvector items per thread, at most
   static_assert(NB <= kThreads && NP <= 64 && 2 * NW <= 128, "one block per thread; one pair per lane");
+  // Branch-free rounds for RM = 40 (one workgroup per CU, registers to
+  // spare); at RM = 24 the unused lanes are masked instead, which keeps the
+  // kernel within the 256 VGPRs of two workgroups per CU.
+  constexpr bool BF = RM > 24;
   const int t = threadIdx.x, lane = t & 63, w = t >> 6;
   const int P = r + (r & 1), NPr = P / 2, NBr = NPr * (NPr + 1) / 2;
   double* part = scratch;  // [NW][2] partial sums
@@ -885,6 +899,7 @@ __device__ __forceinline__ void jacobi_eig(double* Gs, double* G2, double* Ws, d
   const int mr = lane % NPr;
   const int o_pp = at(mr, mr), o_qq = at(P - 1 - mr, P - 1 - mr), o_pq = at(mr, P - 1 - mr);
   const bool blk = t < NBr;
+  const int sink = RM * RM + lane;  // BF: this lane's spare slot (same offset in Gs, G2 and Ws)
   int mi = 0, mk = 0;
   if (blk) {
     mk = (int)((sqrtf(8.0f * (float)t + 1.0f) - 1.0f) * 0.5f);  // t = mk (mk + 1) / 2 + mi
@@ -894,7 +909,10 @@ __device__ __forceinline__ void jacobi_eig(double* Gs, double* G2, double* Ws, d
   }
   const int xi = mi, yi = P - 1 - mi, xk = mk, yk = P - 1 - mk;
   const int r00 = at(xi, xk), r01 = at(xi, yk), r10 = at(yi, xk), r11 = at(yi, yk);
-  const int w00 = at(mv(xi), mv(xk)), w01 = at(mv(xi), mv(yk)), w10 = at(mv(yi), mv(xk)), w11 = at(mv(yi), mv(yk));
+  // BF: threads without a block (and a diagonal block's mirror) store to the sink
+  const bool snk = BF && !blk;
+  const int w00 = snk ? sink : at(mv(xi), mv(xk)), w01 = snk ? sink : at(mv(xi), mv(yk));
+  const int w10 = snk || (BF && mi == mk) ? sink : at(mv(yi), mv(xk)), w11 = snk ? sink : at(mv(yi), mv(yk));
   // eigenvector items (pair m, row c): LDS offsets of (player at position m, c)
   // and (player at position P - 1 - m, c); player 0 never moves
   const int nitem = NPr * P;
@@ -906,15 +924,18 @@ __device__ __forceinline__ void jacobi_eig(double* Gs, double* G2, double* Ws, d
     iv[jj] = e < nitem;
     const int m = iv[jj] ? e / P : 0, c = iv[jj] ? e % P : 0;
     im[jj] = m;
-    op[jj] = m * P + c;
-    oq[jj] = (P - 1 - m) * P + c;
+    op[jj] = BF && !iv[jj] ? sink : m * P + c;  // BF: items beyond nitem read and write the sink
+    oq[jj] = BF && !iv[jj] ? sink : (P - 1 - m) * P + c;
   }
   double* cur = G2;
   double* nxt = Gs;
   auto round = [&](const double* gc, double* gn) __attribute__((always_inline)) {
+    // BF: no branches -- every thread reads valid entries (pair 0's block
+    // when it has none) and stores to its sink what it must not store.
+    // Otherwise the unused loads and stores are skipped by lane masks.
     const double app = gc[o_pp], aqq = gc[o_qq], apq = gc[o_pq];
     double a00 = 0.0, a01 = 0.0, a10 = 0.0, a11 = 0.0;
-    if (blk) {
+    if (BF || blk) {
       a00 = gc[r00];
       a01 = gc[r01];
       a10 = gc[r10];
@@ -924,16 +945,19 @@ __device__ __forceinline__ void jacobi_eig(double* Gs, double* G2, double* Ws, d
 #pragma unroll
     for (int jj = 0; jj < WJ; ++jj) {
       vp[jj] = vq[jj] = 0.0;
-      if (iv[jj]) {
+      if (BF || iv[jj]) {
         vp[jj] = Ws[op[jj]];
         vq[jj] = Ws[oq[jj]];
       }
     }
     double c0, s0;
     jacobi_rotation(app, aqq, apq, c0, s0);
-    if (lane < NPr) wrot[lane] = make_double2(c0, s0);
+    if (BF)
+      wrot[mr] = make_double2(c0, s0);  // lanes >= NP rewrite their pair's slot with the same value
+    else if (lane < NPr)
+      wrot[lane] = make_double2(c0, s0);
     wave_sync();
-    if (blk) {
+    if (BF || blk) {
       const double2 ri = wrot[mi], rk = wrot[mk];
       const double ci = ri.x, si = ri.y, ck = rk.x, sk = rk.y;
       const double b00 = ci * a00 - si * a10, b01 = ci * a01 - si * a11;  // rows: J^T A
@@ -943,18 +967,26 @@ __device__ __forceinline__ void jacobi_eig(double* Gs, double* G2, double* Ws, d
       gn[w00] = n00;
       gn[w01] = n01;
       gn[w11] = n11;
-      if (mi != mk) gn[w10] = n10;  // a diagonal block's (y, x) is its (x, y)
+      if (BF || mi != mk) gn[w10] = n10;  // a diagonal block's (y, x) is its (x, y) (BF: w10 is the sink)
     }
 #pragma unroll
     for (int jj = 0; jj < WJ; ++jj) {
-      if (iv[jj]) {
+      if (BF || iv[jj]) {
         const double2 rm = wrot[im[jj]];
         Ws[op[jj]] = rm.x * vp[jj] - rm.y * vq[jj];
         Ws[oq[jj]] = rm.y * vp[jj] + rm.x * vq[jj];
       }
-      // next round's players: p -> p - 1 (1 -> P - 1), player 0 fixed
-      if (im[jj] != 0) op[jj] = op[jj] < 2 * P ? op[jj] + (P - 2) * P : op[jj] - P;
-      oq[jj] = oq[jj] < 2 * P ? oq[jj] + (P - 2) * P : oq[jj] - P;
+      // next round's players: p -> p - 1 (1 -> P - 1), player 0 fixed (BF:
+      // sinks stay; otherwise an item beyond nitem is never read)
+      const int np = op[jj] < 2 * P ? op[jj] + (P - 2) * P : op[jj] - P;
+      const int nq = oq[jj] < 2 * P ? oq[jj] + (P - 2) * P : oq[jj] - P;
+      if constexpr (BF) {
+        op[jj] = iv[jj] && im[jj] != 0 ? np : op[jj];
+        oq[jj] = iv[jj] ? nq : oq[jj];
+      } else {
+        if (im[jj] != 0) op[jj] = np;
+        oq[jj] = nq;
+      }
     }
     __syncthreads();
   };
