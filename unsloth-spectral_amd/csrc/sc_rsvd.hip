@@ -714,28 +714,56 @@ __device__ __forceinline__ void cholesky_inv_wave(const double* Gs, float* Xf, i
   __syncthreads();
 }
 
+// Sum over the 64 lanes of a wave: DPP quad permutes, row half-mirror and
+// row mirror (every 16-lane row), then permlane32 / permlane16 swaps.
+__device__ __forceinline__ float wave_sum_dpp(float v) {
+  v += __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), 0xB1, 0xF, 0xF, false));
+  v += __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), 0x4E, 0xF, 0xF, false));
+  v += __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), 0x141, 0xF, 0xF, false));
+  v += __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), 0x140, 0xF, 0xF, false));
+  return sum_over_rows(v);
+}
+
 // Columns c < r of Ys [rows][RM] scaled to unit Euclidean norm (a column
-// of zeros stays zero).  Thread t sums column t % RM over rows t / RM,
-// t / RM + G, ... (G = kThreads / RM row groups); the G partial sums of a
-// column are added in a fixed order.  part: >= kThreads floats of scratch.
+// of zeros stays zero; columns >= r are zero).  Thread t holds rows t and
+// t + kThreads in registers; the squares of each column are summed over a
+// wave's lanes with DPP and permlane reductions and over the four waves in
+// a fixed order.  part: >= (kThreads / 64 + 1) * RM floats of scratch.
 template <int RM>
 __device__ __forceinline__ void normalize_cols(float* Ys, int rows, int r, float* part) {
-  constexpr int G = kThreads / RM;
-  const int t = threadIdx.x, c = t % RM, g = t / RM;
-  float s = 0.f;
-  if (g < G && c < r)
-    for (int row = g; row < rows; row += G) s = fmaf(Ys[row * RM + c], Ys[row * RM + c], s);
-  part[t] = s;
-  __syncthreads();
-  if (t < r) {
-    float nn = 0.f;
-    for (int i = 0; i < G; ++i) nn += part[i * RM + t];
-    part[kThreads + t] = nn > 0.f ? 1.0f / sqrtf(nn) : 0.f;
+  static_assert(RM % 4 == 0 && kMaxRows <= 2 * kThreads, "two rows per thread, float4 columns");
+  constexpr int NW = kThreads / 64;
+  const int t = threadIdx.x, lane = t & 63, w = t >> 6;
+  const bool va = t < rows, vb = t + kThreads < rows;
+  float ya[RM], yb[RM];
+#pragma unroll
+  for (int c = 0; c < RM; c += 4) {
+    const float4 a4 = va ? *reinterpret_cast<const float4*>(Ys + t * RM + c) : make_float4(0.f, 0.f, 0.f, 0.f);
+    const float4 b4 = vb ? *reinterpret_cast<const float4*>(Ys + (t + kThreads) * RM + c) : make_float4(0.f, 0.f, 0.f, 0.f);
+    ya[c] = a4.x; ya[c + 1] = a4.y; ya[c + 2] = a4.z; ya[c + 3] = a4.w;
+    yb[c] = b4.x; yb[c + 1] = b4.y; yb[c + 2] = b4.z; yb[c + 3] = b4.w;
+  }
+#pragma unroll
+  for (int c = 0; c < RM; ++c) {
+    const float sq = wave_sum_dpp(fmaf(yb[c], yb[c], ya[c] * ya[c]));
+    if (lane == 0) part[w * RM + c] = sq;
   }
   __syncthreads();
-  for (int e = t; e < rows * RM; e += kThreads) {
-    const int cc = e % RM;
-    if (cc < r) Ys[e] *= part[kThreads + cc];
+  if (t < RM) {
+    float nn = 0.f;
+#pragma unroll
+    for (int ww = 0; ww < NW; ++ww) nn += part[ww * RM + t];
+    part[NW * RM + t] = (t < r && nn > 0.f) ? 1.0f / sqrtf(nn) : 0.f;
+  }
+  __syncthreads();
+#pragma unroll
+  for (int c = 0; c < RM; c += 4) {
+    const float4 s4 = *reinterpret_cast<const float4*>(part + NW * RM + c);
+    if (va)
+      *reinterpret_cast<float4*>(Ys + t * RM + c) = make_float4(ya[c] * s4.x, ya[c + 1] * s4.y, ya[c + 2] * s4.z, ya[c + 3] * s4.w);
+    if (vb)
+      *reinterpret_cast<float4*>(Ys + (t + kThreads) * RM + c) =
+          make_float4(yb[c] * s4.x, yb[c + 1] * s4.y, yb[c + 2] * s4.z, yb[c + 3] * s4.w);
   }
 }
 
