@@ -313,6 +313,39 @@ __device__ __forceinline__ void gemm_rows_mfma(const Job& j, int rows, int cols,
         bl[s][ct][e] = lo;
       }
     }
+  if (rows == kMaxRows && cols == 128) {
+    // the block geometry: a wave's 8 row tiles in two batches of 4, each
+    // batch's loads issued together (two memory round trips, not eight)
+    constexpr int NW = kThreads / 64, BT = 4;
+#pragma unroll 1
+    for (int b0 = 0; b0 < kMaxRows / 16 / NW; b0 += BT) {
+      half8_t a[BT][4];
+#pragma unroll
+      for (int i = 0; i < BT; ++i) {
+        const h16* rp = reinterpret_cast<const h16*>(row_ptr(j, 16 * (w + NW * (b0 + i)) + n, cols));
+#pragma unroll
+        for (int s = 0; s < 4; ++s) a[i][s] = *reinterpret_cast<const half8_t*>(rp + 32 * s + 8 * g);
+      }
+#pragma unroll
+      for (int i = 0; i < BT; ++i) {
+        const int rt = w + NW * (b0 + i);
+#pragma unroll
+        for (int ct = 0; ct < CT; ++ct) {
+          float4_t acc = (float4_t)0.f;
+#pragma unroll
+          for (int s = 0; s < 4; ++s) {
+            acc = __builtin_amdgcn_mfma_f32_16x16x32_f16(a[i][s], bh[s][ct], acc, 0, 0, 0);
+            acc = __builtin_amdgcn_mfma_f32_16x16x32_f16(a[i][s], bl[s][ct], acc, 0, 0, 0);
+          }
+          const int c = 16 * ct + n;
+          if (c < RM)
+#pragma unroll
+            for (int jj = 0; jj < 4; ++jj) Ys[(16 * rt + 4 * g + jj) * RM + c] = acc[jj];
+        }
+      }
+    }
+    return;
+  }
   for (int rt = w; rt < rows / 16; rt += kThreads / 64) {
     const h16* rp = reinterpret_cast<const h16*>(row_ptr(j, 16 * rt + n, cols));
     half8_t a[4];
