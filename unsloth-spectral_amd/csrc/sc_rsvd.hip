@@ -560,7 +560,7 @@ __device__ __forceinline__ void gram_mfma(const float* S, int nrows, int r, doub
       // four independent accumulation chains (rows k0 + 4u + g), summed in
       // a fixed order at the end
       double4_t acc = {0.0, 0.0, 0.0, 0.0}, acc1 = acc, acc2 = acc, acc3 = acc;
-      for (int k0 = 0; k0 < nrows; k0 += 16) {
+      auto step = [&](int k0) __attribute__((always_inline)) {
         double av[4], bv[4];
 #pragma unroll
         for (int u = 0; u < 4; ++u) {
@@ -572,6 +572,13 @@ __device__ __forceinline__ void gram_mfma(const float* S, int nrows, int r, doub
         acc1 = __builtin_amdgcn_mfma_f64_16x16x4f64(av[1], bv[1], acc1, 0, 0, 0);
         acc2 = __builtin_amdgcn_mfma_f64_16x16x4f64(av[2], bv[2], acc2, 0, 0, 0);
         acc3 = __builtin_amdgcn_mfma_f64_16x16x4f64(av[3], bv[3], acc3, 0, 0, 0);
+      };
+      if (RM > 24 && nrows == 128) {
+        // fully unrolled, as in gram_rows_mfma: no loop-carried accumulators
+#pragma unroll
+        for (int k0 = 0; k0 < 128; k0 += 16) step(k0);
+      } else {
+        for (int k0 = 0; k0 < nrows; k0 += 16) step(k0);
       }
       acc = (acc + acc1) + (acc2 + acc3);
 #pragma unroll
@@ -604,8 +611,7 @@ __device__ __forceinline__ void gram_rows_mfma(const float* S, int nrows, int r,
   for (int u = 0; u < 2; ++u)
 #pragma unroll
     for (int ti = 0; ti < NT; ++ti) acc[u][ti] = (double4_t){0.0, 0.0, 0.0, 0.0};
-  const int rpw = nrows / 4;
-  for (int k0 = w * rpw; k0 < (w + 1) * rpw; k0 += 8) {
+  auto step = [&](int k0) __attribute__((always_inline)) {
     double v[2][CT];
 #pragma unroll
     for (int u = 0; u < 2; ++u)
@@ -621,6 +627,16 @@ __device__ __forceinline__ void gram_rows_mfma(const float* S, int nrows, int r,
         for (int tb = ta; tb < CT; ++tb, ++ti)
           acc[u][ti] = __builtin_amdgcn_mfma_f64_16x16x4f64(v[u][ta], v[u][tb], acc[u][ti], 0, 0, 0);
     }
+  };
+  if (RM > 24 && nrows == kMaxRows) {
+    // fully unrolled: no loop-carried accumulators, which the compiler
+    // (MFMA results in AGPRs at one wave per SIMD) would otherwise copy
+    // between the register files around every step
+#pragma unroll
+    for (int i = 0; i < kMaxRows / 32; ++i) step(w * (kMaxRows / 4) + 8 * i);
+  } else {
+    const int rpw = nrows / 4;
+    for (int k0 = w * rpw; k0 < (w + 1) * rpw; k0 += 8) step(k0);
   }
 #pragma unroll
   for (int ti = 0; ti < NT; ++ti) acc[0][ti] = acc[0][ti] + acc[1][ti];
