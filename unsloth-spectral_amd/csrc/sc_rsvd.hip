@@ -138,6 +138,18 @@ __device__ __forceinline__ float2 gauss2(unsigned long long seed, unsigned long 
 }
 
 // ------------------------------------------------------- block helpers
+// p as an opaque LDS address: the accesses of a function then share one base
+// register plus immediate offsets.  Without it the compiler folds every
+// constant element offset into the array's constant address, and where that
+// lies beyond the 64 KB reach of the immediate offset it keeps one address
+// register per element, which spills.
+template <class T>
+__device__ __forceinline__ T* lds_base(T* p) {
+  auto q = (__attribute__((address_space(3))) T*)p;
+  asm volatile("" : "+v"(q));
+  return (T*)q;
+}
+
 template <int RM>
 struct Lds {
   float* Ys;     // [kMaxRows][RM]  Y / Q rows, later the coefficient rows
@@ -295,6 +307,8 @@ __device__ __forceinline__ void split16x8(const float (&v)[8], half8_t& hi, half
 // Ys[rows][RM] = M[rows][cols] Zs[cols][RM]; wave w takes row tiles w, w+4, ...
 template <int RM>
 __device__ __forceinline__ void gemm_rows_mfma(const Job& j, int rows, int cols, const float* Zs, float* Ys) {
+  Zs = lds_base(Zs);
+  Ys = lds_base(Ys);
   constexpr int CT = (RM + 15) / 16;
   const int lane = threadIdx.x & 63, g = lane >> 4, n = lane & 15, w = threadIdx.x >> 6;
   const int KS = cols / 32;
@@ -477,6 +491,9 @@ __device__ __forceinline__ void gemm_cols_mfma(const Job& j, int rows, int cols,
 // gemm_cols_mfma.
 template <int RM>
 __device__ __forceinline__ void gemm_cols_mfma_ct(const Job& j, int rows, const float* Ys, float* Zs, h16* stage) {
+  Ys = lds_base(Ys);
+  Zs = lds_base(Zs);
+  stage = lds_base(stage);
   constexpr int CT = (RM + 15) / 16;
   static_assert(CT == 2 || CT == 3, "two or three column tiles of Ys");
   constexpr int NDT = CT == 2 ? 4 : 8;  // d tiles per wave
@@ -550,6 +567,8 @@ __device__ __forceinline__ void gemm_cols_mfma_ct(const Job& j, int rows, const 
 // (g, n), element e.
 template <int RM>
 __device__ __forceinline__ void gram_mfma(const float* S, int nrows, int r, double* Gs) {
+  S = lds_base(S);
+  Gs = lds_base(Gs);
   constexpr int CT = (RM + 15) / 16;
   const int lane = threadIdx.x & 63, g = lane >> 4, n = lane & 15, w = threadIdx.x >> 6;
   int tix = 0;
@@ -600,6 +619,9 @@ __device__ __forceinline__ void gram_mfma(const float* S, int nrows, int r, doub
 // (w0 + w2) + (w1 + w3).
 template <int RM>
 __device__ __forceinline__ void gram_rows_mfma(const float* S, int nrows, int r, double* Gs, double* slab) {
+  S = lds_base(S);
+  Gs = lds_base(Gs);
+  slab = lds_base(slab);
   constexpr int CT = (RM + 15) / 16;
   constexpr int NT = CT * (CT + 1) / 2;
   static_assert(kThreads == 256, "four waves");
@@ -706,7 +728,11 @@ __device__ __forceinline__ double lane_bcast(double v, int src) {
 template <int RM>
 __device__ __forceinline__ void cholesky_inv_wave(const double* Gs, float* Xf, int r) {
   if (threadIdx.x < 64) {
-    const int lane = threadIdx.x;
+    // The lane index passes through an empty asm so that the per-step lane
+    // masks below are formed in this call, not hoisted out of the caller's
+    // loops as ~2*RM live 64-bit masks (which would spill).
+    int lane = threadIdx.x;
+    asm volatile("" : "+v"(lane));
     const bool act = lane < r;
     double row[RM];
 #pragma unroll
@@ -781,6 +807,8 @@ __device__ __forceinline__ float wave_sum_dpp(float v) {
 template <int RM>
 __device__ __forceinline__ void normalize_cols(float* Ys, int rows, int r, float* part) {
   static_assert(RM % 4 == 0 && kMaxRows <= 2 * kThreads, "two rows per thread, float4 columns");
+  Ys = lds_base(Ys);
+  part = lds_base(part);
   constexpr int NW = kThreads / 64;
   const int t = threadIdx.x, lane = t & 63, w = t >> 6;
   const bool va = t < rows, vb = t + kThreads < rows;
@@ -825,6 +853,8 @@ __device__ __forceinline__ void normalize_cols(float* Ys, int rows, int r, float
 template <int RM>
 __device__ __forceinline__ void apply_rinv(float* Ys, int rows, const float* Xf) {
   static_assert(RM % 4 == 0 && kMaxRows <= 2 * kThreads, "two rows per thread, float4 columns");
+  Ys = lds_base(Ys);
+  Xf = lds_base(Xf);
   const int t = threadIdx.x;
   const bool va = t < rows, vb = t + kThreads < rows;
   float ya[RM], yb[RM];
