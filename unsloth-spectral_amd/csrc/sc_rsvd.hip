@@ -22,6 +22,8 @@
 // zeroed, so rank-deficient blocks (zeros, repeated rows) stay finite.
 #include <math.h>
 
+#include <utility>
+
 #include "sc_common.h"
 
 namespace {
@@ -717,13 +719,79 @@ __device__ __forceinline__ double lane_bcast(double v, int src) {
   return __longlong_as_double(((long long)hi << 32) | (unsigned)lo);
 }
 
+// Step JC of the Cholesky factorisation in cholesky_inv_wave: lane i holds
+// row i of the trailing matrix; column JC is scaled by the pivot and the
+// rank-1 update applied to the columns after it.  The broadcasts of L[k][JC]
+// go in groups of 8, each group's readlanes issued before its FMAs (one
+// SGPR pair per value, no stall between a readlane and its use).
+template <int RM, int JC>
+__device__ __forceinline__ void chol_col(double (&row)[RM], int lane, int r, double tol, double& il_own) {
+  if (JC >= r) return;  // wave-uniform
+  const double piv = lane_bcast(row[JC], JC);
+  const bool dead = !(piv > tol);
+  const double il = dead ? 0.0 : rsqrt64(piv);
+  if (lane > JC) row[JC] *= il;                     // L[lane][JC]
+  if (lane == JC) {
+    row[JC] = dead ? 0.0 : piv * il;                // L[JC][JC] = sqrt(piv)
+    il_own = il;
+  }
+  // the multiplier is zeroed on lanes <= JC, so the FMAs need no select
+  const double lm = lane > JC ? -row[JC] : 0.0;
+#pragma unroll
+  for (int k0 = (JC + 1) & ~7; k0 < RM; k0 += 8) {
+    double lk[8];
+#pragma unroll
+    for (int u = 0; u < 8; ++u)
+      if (k0 + u > JC && k0 + u < RM) lk[u] = lane_bcast(row[JC], k0 + u);  // L[k][JC]
+    __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+    for (int u = 0; u < 8; ++u)
+      if (k0 + u > JC && k0 + u < RM) row[k0 + u] = fma(lm, lk[u], row[k0 + u]);
+  }
+}
+
+// Step M of the forward substitution in cholesky_inv_wave: lane M finishes
+// its row of L^{-1}; the lanes after it subtract L[lane][M] times that row.
+template <int RM, int M>
+__device__ __forceinline__ void inv_row(double (&y)[RM], const double (&row)[RM], int lane, double il_own) {
+  if (lane == M) {
+#pragma unroll
+    for (int n = 0; n <= M; ++n) y[n] = ((n == M ? 1.0 : 0.0) - y[n]) * il_own;
+  }
+  const double lim = lane > M ? row[M] : 0.0;  // L[lane][M]; 0 leaves the finished rows unchanged
+#pragma unroll
+  for (int n0 = 0; n0 <= M; n0 += 8) {
+    double ym[8];
+#pragma unroll
+    for (int u = 0; u < 8; ++u)
+      if (n0 + u <= M) ym[u] = lane_bcast(y[n0 + u], M);
+    __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+    for (int u = 0; u < 8; ++u)
+      if (n0 + u <= M) y[n0 + u] = fma(lim, ym[u], y[n0 + u]);
+  }
+}
+
+// The steps as one fold over a compile-time index sequence (straight-line
+// code with static register indices, not a loop left to the unroller).
+template <int RM, int... J>
+__device__ __forceinline__ void chol_cols(double (&row)[RM], int lane, int r, double tol, double& il_own,
+                                          std::integer_sequence<int, J...>) {
+  (chol_col<RM, J>(row, lane, r, tol, il_own), ...);
+}
+template <int RM, int... M>
+__device__ __forceinline__ void inv_rows(double (&y)[RM], const double (&row)[RM], int lane, double il_own,
+                                         std::integer_sequence<int, M...>) {
+  (inv_row<RM, M>(y, row, lane, il_own), ...);
+}
+
 // Cholesky G = L L^T of Gs (r x r, r <= RM) and X = R^{-1} with R = L^T, by
-// wave 0.  Lane i keeps row i of L in registers; the steps are unrolled, so
-// register indices are static, and values move between lanes by readlane
-// (no LDS, no barrier inside).  Dead columns (pivot <= 1e-26 of the largest
-// diagonal entry) get L[:, j] = 0 and X[:, j] = 0.  Then lane i forms row i
-// of L^{-1} by forward substitution against the rows of the lanes before it,
-// and writes it as column i of X (fp32, row-major [RM][RM], upper
+// wave 0.  Lane i keeps row i of L in registers; the steps are straight-line
+// code, so register indices are static, and values move between lanes by
+// readlane (no LDS, no barrier inside).  Dead columns (pivot <= 1e-26 of the
+// largest diagonal entry) get L[:, j] = 0 and X[:, j] = 0.  Then lane i forms
+// row i of L^{-1} by forward substitution against the rows of the lanes
+// before it, and writes it as column i of X (fp32, row-major [RM][RM], upper
 // triangular) into Xf.
 template <int RM>
 __device__ __forceinline__ void cholesky_inv_wave(const double* Gs, float* Xf, int r) {
@@ -742,44 +810,12 @@ __device__ __forceinline__ void cholesky_inv_wave(const double* Gs, float* Xf, i
     for (int k = 0; k < RM; ++k) gm = fmax(gm, lane_bcast(row[k], k));
     const double tol = gm * 1e-26 + 1e-300;
     double il_own = 0.0;  // 1 / L[lane][lane] (0 when dead)
-#pragma unroll
-    for (int jc = 0; jc < RM; ++jc) {
-      if (jc < r) {  // wave-uniform
-        const double piv = lane_bcast(row[jc], jc);
-        const bool dead = !(piv > tol);
-        const double il = dead ? 0.0 : rsqrt64(piv);
-        if (lane > jc) row[jc] *= il;                     // L[lane][jc]
-        if (lane == jc) {
-          row[jc] = dead ? 0.0 : piv * il;                // L[jc][jc] = sqrt(piv)
-          il_own = il;
-        }
-        // the trailing update with the multiplier zeroed on lanes <= jc, so
-        // the FMAs need no per-element select
-        const double lm = lane > jc ? -row[jc] : 0.0;
-#pragma unroll
-        for (int k = jc + 1; k < RM; ++k) {
-          const double lk = lane_bcast(row[jc], k);       // L[k][jc]
-          row[k] = fma(lm, lk, row[k]);
-        }
-      }
-    }
+    chol_cols<RM>(row, lane, r, tol, il_own, std::make_integer_sequence<int, RM>{});
     // y = row `lane` of L^{-1}: y[n] = (delta(lane, n) - sum_{m<lane} L[lane][m] Y[m][n]) / L[lane][lane]
     double y[RM];
 #pragma unroll
     for (int n = 0; n < RM; ++n) y[n] = 0.0;
-#pragma unroll
-    for (int m = 0; m < RM; ++m) {
-      if (lane == m) {
-#pragma unroll
-        for (int n = 0; n <= m; ++n) y[n] = ((n == m ? 1.0 : 0.0) - y[n]) * il_own;
-      }
-      const double lim = lane > m ? row[m] : 0.0;  // L[lane][m]; 0 leaves the finished rows unchanged
-#pragma unroll
-      for (int n = 0; n <= m; ++n) {
-        const double ymn = lane_bcast(y[n], m);
-        y[n] = fma(lim, ymn, y[n]);
-      }
-    }
+    inv_rows<RM>(y, row, lane, il_own, std::make_integer_sequence<int, RM>{});
     // X[n][lane] = Y[lane][n]
     if (lane < RM) {
 #pragma unroll
