@@ -711,6 +711,39 @@ __device__ __forceinline__ double rsqrt64(double x) {
   return y * fma(-0.5 * x * y, y, 1.5);
 }
 
+// A double moved across lanes by the DPP control CTRL (both halves).
+template <int CTRL>
+__device__ __forceinline__ double dpp_d(double v) {
+  const long long u = __double_as_longlong(v);
+  const int lo = __builtin_amdgcn_update_dpp(0, (int)(u & 0xffffffffLL), CTRL, 0xF, 0xF, false);
+  const int hi = __builtin_amdgcn_update_dpp(0, (int)(u >> 32), CTRL, 0xF, 0xF, false);
+  return __longlong_as_double(((long long)hi << 32) | (unsigned)lo);
+}
+
+// op over the 64 lanes of a wave for doubles, the result in every lane: DPP
+// quad permutes, row half-mirror and row mirror (every 16-lane row), then
+// permlane32 / permlane16 swaps between rows (VALU only, no LDS).
+template <class Op>
+__device__ __forceinline__ double wave_reduce_d(double v, Op op) {
+  v = op(v, dpp_d<0xB1>(v));
+  v = op(v, dpp_d<0x4E>(v));
+  v = op(v, dpp_d<0x141>(v));
+  v = op(v, dpp_d<0x140>(v));
+  auto swap_op = [&](double x, bool wide) __attribute__((always_inline)) {
+    const long long u = __double_as_longlong(x);
+    const uint32_t lo = (uint32_t)(u & 0xffffffffLL), hi = (uint32_t)(u >> 32);
+    auto a = wide ? __builtin_amdgcn_permlane32_swap(lo, lo, false, false)
+                  : __builtin_amdgcn_permlane16_swap(lo, lo, false, false);
+    auto b = wide ? __builtin_amdgcn_permlane32_swap(hi, hi, false, false)
+                  : __builtin_amdgcn_permlane16_swap(hi, hi, false, false);
+    const double x0 = __longlong_as_double(((long long)b[0] << 32) | a[0]);
+    const double x1 = __longlong_as_double(((long long)b[1] << 32) | a[1]);
+    return op(x0, x1);
+  };
+  v = swap_op(v, true);
+  return swap_op(v, false);
+}
+
 // Wave-uniform copy of lane `src`'s double (src a compile-time or uniform index).
 __device__ __forceinline__ double lane_bcast(double v, int src) {
   const long long u = __double_as_longlong(v);
@@ -750,25 +783,31 @@ __device__ __forceinline__ void chol_col(double (&row)[RM], int lane, int r, dou
   }
 }
 
-// Step M of the forward substitution in cholesky_inv_wave: lane M finishes
-// its row of L^{-1}; the lanes after it subtract L[lane][M] times that row.
+// Step M of the forward substitution in cholesky_inv_wave, for the columns
+// n = 4 j + w of L^{-1} that wave w computes (y[j] = L^{-1}[lane][n]):
+// lane M finishes its entries; the lanes after it subtract L[lane][M]
+// times them.  Entries with n > M are still zero, so only j <= M / 4 can
+// carry anything (a zero broadcast where 4 j + w > M adds nothing).
 template <int RM, int M>
-__device__ __forceinline__ void inv_row(double (&y)[RM], const double (&row)[RM], int lane, double il_own) {
+__device__ __forceinline__ void inv_row(double (&y)[RM / 4], const double (&row)[RM], int lane, int w, int r,
+                                        double il_own) {
+  if (M >= r) return;  // wave-uniform: rows r.. of L are zero, their rows of L^{-1} too
+  constexpr int JM = M / 4;
   if (lane == M) {
 #pragma unroll
-    for (int n = 0; n <= M; ++n) y[n] = ((n == M ? 1.0 : 0.0) - y[n]) * il_own;
+    for (int j = 0; j <= JM; ++j) y[j] = ((4 * j + w == M ? 1.0 : 0.0) - y[j]) * il_own;
   }
   const double lim = lane > M ? row[M] : 0.0;  // L[lane][M]; 0 leaves the finished rows unchanged
 #pragma unroll
-  for (int n0 = 0; n0 <= M; n0 += 8) {
+  for (int j0 = 0; j0 <= JM; j0 += 8) {
     double ym[8];
 #pragma unroll
     for (int u = 0; u < 8; ++u)
-      if (n0 + u <= M) ym[u] = lane_bcast(y[n0 + u], M);
+      if (j0 + u <= JM) ym[u] = lane_bcast(y[j0 + u], M);
     __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
     for (int u = 0; u < 8; ++u)
-      if (n0 + u <= M) y[n0 + u] = fma(lim, ym[u], y[n0 + u]);
+      if (j0 + u <= JM) y[j0 + u] = fma(lim, ym[u], y[j0 + u]);
   }
 }
 
@@ -780,46 +819,68 @@ __device__ __forceinline__ void chol_cols(double (&row)[RM], int lane, int r, do
   (chol_col<RM, J>(row, lane, r, tol, il_own), ...);
 }
 template <int RM, int... M>
-__device__ __forceinline__ void inv_rows(double (&y)[RM], const double (&row)[RM], int lane, double il_own,
-                                         std::integer_sequence<int, M...>) {
-  (inv_row<RM, M>(y, row, lane, il_own), ...);
+__device__ __forceinline__ void inv_rows(double (&y)[RM / 4], const double (&row)[RM], int lane, int w, int r,
+                                         double il_own, std::integer_sequence<int, M...>) {
+  (inv_row<RM, M>(y, row, lane, w, r, il_own), ...);
 }
 
-// Cholesky G = L L^T of Gs (r x r, r <= RM) and X = R^{-1} with R = L^T, by
-// wave 0.  Lane i keeps row i of L in registers; the steps are straight-line
-// code, so register indices are static, and values move between lanes by
-// readlane (no LDS, no barrier inside).  Dead columns (pivot <= 1e-26 of the
-// largest diagonal entry) get L[:, j] = 0 and X[:, j] = 0.  Then lane i forms
-// row i of L^{-1} by forward substitution against the rows of the lanes
-// before it, and writes it as column i of X (fp32, row-major [RM][RM], upper
-// triangular) into Xf.
+// Cholesky G = L L^T of Gs (r x r, r <= RM) and X = R^{-1} with R = L^T.
+// Wave 0 factorises: lane i keeps row i of L in registers; the steps are
+// straight-line code, so register indices are static, and values move
+// between lanes by readlane (no LDS, no barrier inside).  Dead columns
+// (pivot <= 1e-26 of the largest diagonal entry) get L[:, j] = 0 and
+// X[:, j] = 0.  L goes to LDS (transposed, over Gs) with 1 / L[i][i] in
+// ilbuf; then every wave reloads it and wave w forms the columns n = 4 j + w
+// of L^{-1}, lane i its row i, by forward substitution against the rows of
+// the lanes before it (each element sees the same operations in the same
+// order as a one-wave substitution), and writes them as column i of X
+// (fp32, row-major [RM][RM], upper triangular) into Xf.
 template <int RM>
-__device__ __forceinline__ void cholesky_inv_wave(const double* Gs, float* Xf, int r) {
+__device__ __forceinline__ void cholesky_inv_wave(double* Gs, float* Xf, double* ilbuf, int r) {
+  static_assert(RM % 4 == 0 && kThreads == 256, "four waves, RM / 4 columns each");
+  // The lane index passes through an empty asm so that the per-step lane
+  // masks below are formed in this call, not hoisted out of the caller's
+  // loops as ~2*RM live 64-bit masks (which would spill).
+  int lane = threadIdx.x & 63;
+  asm volatile("" : "+v"(lane));
+  const bool act = lane < r;
   if (threadIdx.x < 64) {
-    // The lane index passes through an empty asm so that the per-step lane
-    // masks below are formed in this call, not hoisted out of the caller's
-    // loops as ~2*RM live 64-bit masks (which would spill).
-    int lane = threadIdx.x;
-    asm volatile("" : "+v"(lane));
-    const bool act = lane < r;
     double row[RM];
 #pragma unroll
     for (int k = 0; k < RM; ++k) row[k] = (act && k < r) ? Gs[lane * RM + k] : 0.0;
-    double gm = 0.0;
-#pragma unroll
-    for (int k = 0; k < RM; ++k) gm = fmax(gm, lane_bcast(row[k], k));
+    // largest diagonal entry (the diagonal read once more from LDS: a
+    // lane's own entry sits at a lane-dependent register index)
+    const double gm = wave_reduce_d(act ? Gs[lane * RM + lane] : 0.0,
+                                    [](double a, double b) __attribute__((always_inline)) { return fmax(a, b); });
     const double tol = gm * 1e-26 + 1e-300;
     double il_own = 0.0;  // 1 / L[lane][lane] (0 when dead)
     chol_cols<RM>(row, lane, r, tol, il_own, std::make_integer_sequence<int, RM>{});
-    // y = row `lane` of L^{-1}: y[n] = (delta(lane, n) - sum_{m<lane} L[lane][m] Y[m][n]) / L[lane][lane]
-    double y[RM];
-#pragma unroll
-    for (int n = 0; n < RM; ++n) y[n] = 0.0;
-    inv_rows<RM>(y, row, lane, il_own, std::make_integer_sequence<int, RM>{});
-    // X[n][lane] = Y[lane][n]
+    wave_sync();  // every lane's reads of Gs are done
     if (lane < RM) {
 #pragma unroll
-      for (int n = 0; n < RM; ++n) Xf[n * RM + lane] = (act && n <= lane) ? (float)y[n] : 0.f;
+      for (int k = 0; k < RM; ++k) Gs[k * RM + lane] = row[k];  // L^T: lane-consecutive, no bank conflicts
+      ilbuf[lane] = il_own;
+    }
+  }
+  __syncthreads();
+  {
+    const int w = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    double row[RM];
+#pragma unroll
+    for (int k = 0; k < RM; ++k) row[k] = lane < RM ? Gs[k * RM + min(lane, RM - 1)] : 0.0;
+    const double il_own = lane < RM ? ilbuf[min(lane, RM - 1)] : 0.0;
+    // y[j] = L^{-1}[lane][4 j + w]: (delta(lane, n) - sum_{m<lane} L[lane][m] L^{-1}[m][n]) / L[lane][lane]
+    double y[RM / 4];
+#pragma unroll
+    for (int j = 0; j < RM / 4; ++j) y[j] = 0.0;
+    inv_rows<RM>(y, row, lane, w, r, il_own, std::make_integer_sequence<int, RM>{});
+    // X[n][lane] = L^{-1}[lane][n]
+    if (lane < RM) {
+#pragma unroll
+      for (int j = 0; j < RM / 4; ++j) {
+        const int n = 4 * j + w;
+        Xf[n * RM + lane] = (act && n <= lane) ? (float)y[j] : 0.f;
+      }
     }
   }
   __syncthreads();
@@ -1144,11 +1205,9 @@ __device__ __forceinline__ void jacobi_eig(double* Gs, double* G2, double* Ws, d
       else if (i < k)
         off += 2.0 * (v * v);
     }
-#pragma unroll
-    for (int o = 32; o > 0; o >>= 1) {
-      off += __shfl_xor(off, o);
-      dia += __shfl_xor(dia, o);
-    }
+    auto add = [](double a, double b) __attribute__((always_inline)) { return a + b; };
+    off = wave_reduce_d(off, add);
+    dia = wave_reduce_d(dia, add);
     if (lane == 0) {
       part[2 * w] = off;
       part[2 * w + 1] = dia;
@@ -1228,7 +1287,7 @@ __device__ __forceinline__ void run_matrix(const RsvdParams& p, const Job& j, in
       __syncthreads();
       gram_rows_mfma<RM>(L.Ys, rows, r, L.Gs, reinterpret_cast<double*>(L.Zs));  // Zs, Wf: dead here
       __syncthreads();
-      cholesky_inv_wave<RM>(L.Gs, L.Wf, r);
+      cholesky_inv_wave<RM>(L.Gs, L.Wf, L.red, r);  // red: dead here
       apply_rinv<RM>(L.Ys, rows, L.Wf);
     }
   };
@@ -1266,18 +1325,19 @@ __device__ __forceinline__ void run_matrix(const RsvdParams& p, const Job& j, in
   if (t < r) {
     const double lc = L.Gs[t * RM + t];
     int rank = 0;
-    for (int b2 = 0; b2 < r; ++b2) {
+#pragma unroll
+    for (int b2 = 0; b2 < RM; ++b2) {  // every load in flight at once; b2 >= r masked
       const double lb = L.Gs[b2 * RM + b2];
-      rank += (lb > lc) || (lb == lc && b2 < t);
+      rank += b2 < r && ((lb > lc) || (lb == lc && b2 < t));
     }
     L.ord[rank] = t;
   }
   __syncthreads();
-  // Wf[c][i] = W[c][ord_i] * S_i  (i < k; 0 for k <= i < RM)
-  for (int e = t; e < r * RM; e += kThreads) {
+  // Wf[c][i] = W[c][ord_i] * S_i  (c < r, i < k; 0 elsewhere)
+  for (int e = t; e < RM * RM; e += kThreads) {
     const int c = e / RM, i = e % RM;
     float v = 0.f;
-    if (i < k) {
+    if (c < r && i < k) {
       const int oi = L.ord[i];
       v = (float)(L.Ws[oi * P + c] * sqrt(fmax(L.Gs[oi * RM + oi], 0.0)));
     }
@@ -1287,19 +1347,48 @@ __device__ __forceinline__ void run_matrix(const RsvdParams& p, const Job& j, in
   // ---- coefficients, in place over the Q rows of Ys: Ys[row][i] =
   // sum_c Q[row][c] Wf[c][i] (0 for k <= i < RM), divided by the row weight
   // when weighted.  Thread t reads and overwrites only its own rows t and
-  // t + kThreads; c runs in a runtime loop and each float4 of Wf (a wave
-  // broadcast) serves both rows.
+  // t + kThreads; each float4 of Wf (a wave broadcast) serves both rows
+  // (Q's columns >= r and Wf's rows >= r are zero).
   const bool v0 = t < rows, v1 = t + kThreads < rows;
   {
     float cf0[RM], cf1[RM];
 #pragma unroll
     for (int i = 0; i < RM; ++i) cf0[i] = cf1[i] = 0.f;
+    if constexpr (RM <= 24) {
+      // four columns per step: two float4 row loads and 4 x RM / 4 Wf loads
+      // in flight together
+      const float* ya = lds_base(L.Ys) + t * RM;
+      const float* wf = lds_base(L.Wf);
 #pragma unroll 1
-    for (int c = 0; c < r; ++c) {
-      const float q0 = v0 ? L.Ys[t * RM + c] : 0.f, q1 = v1 ? L.Ys[(t + kThreads) * RM + c] : 0.f;
+      for (int c4 = 0; c4 < RM; c4 += 4) {
+        const float4 a4 = *reinterpret_cast<const float4*>(ya + c4);  // rows t, t + kThreads < kMaxRows: in bounds
+        const float4 b4 = *reinterpret_cast<const float4*>(ya + kThreads * RM + c4);
+        const float qa[4] = {v0 ? a4.x : 0.f, v0 ? a4.y : 0.f, v0 ? a4.z : 0.f, v0 ? a4.w : 0.f};
+        const float qb[4] = {v1 ? b4.x : 0.f, v1 ? b4.y : 0.f, v1 ? b4.z : 0.f, v1 ? b4.w : 0.f};
 #pragma unroll
-      for (int i = 0; i < RM; i += 4) {
-        {  // all RM columns: Wf[c][i] = 0 for i >= k, so those accumulators stay 0 (no branches)
+        for (int u = 0; u < 4; ++u) {
+          const float q0 = qa[u], q1 = qb[u];
+#pragma unroll
+          for (int i = 0; i < RM; i += 4) {  // Wf[c][i] = 0 for i >= k: those accumulators stay 0
+            const float4 w = *reinterpret_cast<const float4*>(wf + (c4 + u) * RM + i);
+            cf0[i] = fmaf(q0, w.x, cf0[i]);
+            cf0[i + 1] = fmaf(q0, w.y, cf0[i + 1]);
+            cf0[i + 2] = fmaf(q0, w.z, cf0[i + 2]);
+            cf0[i + 3] = fmaf(q0, w.w, cf0[i + 3]);
+            cf1[i] = fmaf(q1, w.x, cf1[i]);
+            cf1[i + 1] = fmaf(q1, w.y, cf1[i + 1]);
+            cf1[i + 2] = fmaf(q1, w.z, cf1[i + 2]);
+            cf1[i + 3] = fmaf(q1, w.w, cf1[i + 3]);
+          }
+        }
+      }
+    } else {
+      // one column per step (fewer registers in flight at RM = 40)
+#pragma unroll 1
+      for (int c = 0; c < r; ++c) {
+        const float q0 = v0 ? L.Ys[t * RM + c] : 0.f, q1 = v1 ? L.Ys[(t + kThreads) * RM + c] : 0.f;
+#pragma unroll
+        for (int i = 0; i < RM; i += 4) {  // Wf[c][i] = 0 for i >= k: those accumulators stay 0
           const float4 w = *reinterpret_cast<const float4*>(L.Wf + c * RM + i);
           cf0[i] = fmaf(q0, w.x, cf0[i]);
           cf0[i + 1] = fmaf(q0, w.y, cf0[i + 1]);
@@ -1375,8 +1464,7 @@ __device__ __forceinline__ void run_matrix(const RsvdParams& p, const Job& j, in
       const double v = L.Zs[i * cols + d];
       nn += v * v;
     }
-#pragma unroll
-    for (int o = 32; o > 0; o >>= 1) nn += __shfl_xor(nn, o);
+    nn = wave_reduce_d(nn, [](double a, double b) __attribute__((always_inline)) { return a + b; });
     if ((t & 63) == 0) {
       L.red[i] = nn > 0.0 ? 1.0 / sqrt(nn) : 0.0;
       if (p.svals_out && dbg_index >= 0) {
