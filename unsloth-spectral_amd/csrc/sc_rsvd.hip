@@ -509,51 +509,60 @@ __device__ __forceinline__ void gemm_cols_mfma_ct(const Job& j, int rows, const 
 #pragma unroll
   for (int dt = 0; dt < NDT; ++dt) acc[dt] = (float4_t)0.f;
   const int c0 = t, c1 = t + kThreads;
-  uint4 nx0, nx1;
-  auto fetch = [&](int k0) __attribute__((always_inline)) {
-    nx0 = *reinterpret_cast<const uint4*>(row_ptr(j, k0 + c0 / cpr, cols) + (c0 % cpr) * 16);
-    nx1 = *reinterpret_cast<const uint4*>(row_ptr(j, k0 + c1 / cpr, cols) + (c1 % cpr) * 16);
+  // up to two tiles of M in flight in registers beyond the staged one
+  uint4 nx0, nx1, nn0, nn1;
+  auto fetch = [&](int k0, uint4& x0, uint4& x1) __attribute__((always_inline)) {
+    x0 = *reinterpret_cast<const uint4*>(row_ptr(j, k0 + c0 / cpr, cols) + (c0 % cpr) * 16);
+    x1 = *reinterpret_cast<const uint4*>(row_ptr(j, k0 + c1 / cpr, cols) + (c1 % cpr) * 16);
   };
-  auto put = [&]() __attribute__((always_inline)) {
-    *reinterpret_cast<uint4*>(stage + (c0 / cpr) * pitch + (c0 % cpr) * 8) = nx0;
-    *reinterpret_cast<uint4*>(stage + (c1 / cpr) * pitch + (c1 % cpr) * 8) = nx1;
+  auto put = [&](const uint4& x0, const uint4& x1) __attribute__((always_inline)) {
+    *reinterpret_cast<uint4*>(stage + (c0 / cpr) * pitch + (c0 % cpr) * 8) = x0;
+    *reinterpret_cast<uint4*>(stage + (c1 / cpr) * pitch + (c1 % cpr) * 8) = x1;
   };
-  fetch(0);
-  put();
+  fetch(0, nx0, nx1);
+  if (kColTile < rows) fetch(kColTile, nn0, nn1);
+  put(nx0, nx1);
   __syncthreads();
-  for (int k0 = 0; k0 < rows; k0 += kColTile) {
+  // step(k0, a, b): b holds tile k0 + kColTile (in flight), a is free and
+  // receives tile k0 + 2 kColTile; two steps per iteration swap the roles
+  // (no register copies, which would wait for the loads)
+  auto step = [&](int k0, uint4& a0, uint4& a1, const uint4& b0, const uint4& b1) __attribute__((always_inline)) {
     const bool more = k0 + kColTile < rows;
-    if (more) fetch(k0 + kColTile);
+    if (k0 + 2 * kColTile < rows) fetch(k0 + 2 * kColTile, a0, a1);
     if (busy) {
-    half8_t a[NDT];
+      half8_t a[NDT];
 #pragma unroll
-    for (int dt = 0; dt < NDT; ++dt) {
-      const h16* p0 = stage + (8 * g + (n >> 2)) * pitch + (dt0 + dt) * 16 + 4 * (n & 3);
-      typedef __attribute__((address_space(3))) short4_t lds_s4;
-      const short4_t lo = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_s4*)(p0));
-      const short4_t hi = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_s4*)(p0 + 4 * pitch));
-      const half4_t l4 = __builtin_bit_cast(half4_t, lo), h4 = __builtin_bit_cast(half4_t, hi);
-      a[dt] = (half8_t){l4.x, l4.y, l4.z, l4.w, h4.x, h4.y, h4.z, h4.w};
-    }
-    float yv[8];
+      for (int dt = 0; dt < NDT; ++dt) {
+        const h16* p0 = stage + (8 * g + (n >> 2)) * pitch + (dt0 + dt) * 16 + 4 * (n & 3);
+        typedef __attribute__((address_space(3))) short4_t lds_s4;
+        const short4_t lo = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_s4*)(p0));
+        const short4_t hi = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_s4*)(p0 + 4 * pitch));
+        const half4_t l4 = __builtin_bit_cast(half4_t, lo), h4 = __builtin_bit_cast(half4_t, hi);
+        a[dt] = (half8_t){l4.x, l4.y, l4.z, l4.w, h4.x, h4.y, h4.z, h4.w};
+      }
+      float yv[8];
 #pragma unroll
-    for (int e = 0; e < 8; ++e) {
-      const float y = Ys[(k0 + 8 * g + e) * RM + min(c, RM - 1)];  // in bounds: no exec branch
-      yv[e] = c < RM ? y : 0.f;
-    }
-    half8_t bh, bl;
-    split16x8(yv, bh, bl);
+      for (int e = 0; e < 8; ++e) {
+        const float y = Ys[(k0 + 8 * g + e) * RM + min(c, RM - 1)];  // in bounds: no exec branch
+        yv[e] = c < RM ? y : 0.f;
+      }
+      half8_t bh, bl;
+      split16x8(yv, bh, bl);
 #pragma unroll
-    for (int dt = 0; dt < NDT; ++dt) {
-      acc[dt] = __builtin_amdgcn_mfma_f32_16x16x32_f16(a[dt], bh, acc[dt], 0, 0, 0);
-      acc[dt] = __builtin_amdgcn_mfma_f32_16x16x32_f16(a[dt], bl, acc[dt], 0, 0, 0);
-    }
+      for (int dt = 0; dt < NDT; ++dt) {
+        acc[dt] = __builtin_amdgcn_mfma_f32_16x16x32_f16(a[dt], bh, acc[dt], 0, 0, 0);
+        acc[dt] = __builtin_amdgcn_mfma_f32_16x16x32_f16(a[dt], bl, acc[dt], 0, 0, 0);
+      }
     }
     __syncthreads();  // every wave is done with this tile
     if (more) {
-      put();
+      put(b0, b1);
       __syncthreads();
     }
+  };
+  for (int k0 = 0; k0 < rows; k0 += 2 * kColTile) {
+    step(k0, nx0, nx1, nn0, nn1);
+    if (k0 + kColTile < rows) step(k0 + kColTile, nn0, nn1, nx0, nx1);
   }
   if (busy && c < RM)
 #pragma unroll
@@ -652,10 +661,11 @@ __device__ __forceinline__ void gram_rows_mfma(const float* S, int nrows, int r,
           acc[u][ti] = __builtin_amdgcn_mfma_f64_16x16x4f64(v[u][ta], v[u][tb], acc[u][ti], 0, 0, 0);
     }
   };
-  if (RM > 24 && nrows == kMaxRows) {
-    // fully unrolled: no loop-carried accumulators, which the compiler
-    // (MFMA results in AGPRs at one wave per SIMD) would otherwise copy
-    // between the register files around every step
+  if (nrows == kMaxRows) {
+    // fully unrolled: every step's loads can be issued ahead of the MFMAs
+    // before them, and no accumulator is loop-carried (at one wave per
+    // SIMD the compiler would copy loop-carried MFMA results between the
+    // register files around every step)
 #pragma unroll
     for (int i = 0; i < kMaxRows / 32; ++i) step(w * (kMaxRows / 4) + 8 * i);
   } else {
