@@ -1144,25 +1144,18 @@ __device__ __forceinline__ void jacobi_eig(double* Gs, double* G2, double* Ws, d
   double* cur = G2;
   double* nxt = Gs;
   auto round = [&](const double* gc, double* gn) __attribute__((always_inline)) {
-    // BF: no branches -- every thread reads valid entries (pair 0's block
-    // when it has none) and stores to its sink what it must not store.
-    // Otherwise the unused loads and stores are skipped by lane masks.
+    // Every load is unconditional (a thread without a block reads pair 0's,
+    // an item beyond the last reads offset 0), so each round has two LDS
+    // round trips: the entries, then the rotations.  BF: no branches at all
+    // -- what a thread must not store goes to its sink.  Otherwise the
+    // unused stores are skipped by lane masks.
     const double app = gc[o_pp], aqq = gc[o_qq], apq = gc[o_pq];
-    double a00 = 0.0, a01 = 0.0, a10 = 0.0, a11 = 0.0;
-    if (BF || blk) {
-      a00 = gc[r00];
-      a01 = gc[r01];
-      a10 = gc[r10];
-      a11 = gc[r11];
-    }
+    const double a00 = gc[r00], a01 = gc[r01], a10 = gc[r10], a11 = gc[r11];
     double vp[WJ], vq[WJ];
 #pragma unroll
     for (int jj = 0; jj < WJ; ++jj) {
-      vp[jj] = vq[jj] = 0.0;
-      if (BF || iv[jj]) {
-        vp[jj] = Ws[op[jj]];
-        vq[jj] = Ws[oq[jj]];
-      }
+      vp[jj] = Ws[op[jj]];
+      vq[jj] = Ws[oq[jj]];
     }
     double c0, s0;
     jacobi_rotation(app, aqq, apq, c0, s0);
@@ -1171,27 +1164,32 @@ __device__ __forceinline__ void jacobi_eig(double* Gs, double* G2, double* Ws, d
     else if (lane < NPr)
       wrot[lane] = make_double2(c0, s0);
     wave_sync();
-    if (BF || blk) {
-      const double2 ri = wrot[mi], rk = wrot[mk];
+    const double2 ri = wrot[mi], rk = wrot[mk];
+    double2 rm[WJ];
+#pragma unroll
+    for (int jj = 0; jj < WJ; ++jj) rm[jj] = wrot[im[jj]];
+    {
       const double ci = ri.x, si = ri.y, ck = rk.x, sk = rk.y;
       const double b00 = ci * a00 - si * a10, b01 = ci * a01 - si * a11;  // rows: J^T A
       const double b10 = si * a00 + ci * a10, b11 = si * a01 + ci * a11;
       const double n00 = ck * b00 - sk * b01, n01 = sk * b00 + ck * b01;  // columns: (J^T A) J
       const double n10 = ck * b10 - sk * b11, n11 = sk * b10 + ck * b11;
-      gn[w00] = n00;
-      gn[w01] = n01;
-      gn[w11] = n11;
-      if (BF || mi != mk) gn[w10] = n10;  // a diagonal block's (y, x) is its (x, y) (BF: w10 is the sink)
+      if (BF || blk) {
+        gn[w00] = n00;
+        gn[w01] = n01;
+        gn[w11] = n11;
+        if (BF || mi != mk) gn[w10] = n10;  // a diagonal block's (y, x) is its (x, y) (BF: w10 is the sink)
+      }
     }
 #pragma unroll
     for (int jj = 0; jj < WJ; ++jj) {
       if (BF || iv[jj]) {
-        const double2 rm = wrot[im[jj]];
-        Ws[op[jj]] = rm.x * vp[jj] - rm.y * vq[jj];
-        Ws[oq[jj]] = rm.y * vp[jj] + rm.x * vq[jj];
+        Ws[op[jj]] = rm[jj].x * vp[jj] - rm[jj].y * vq[jj];
+        Ws[oq[jj]] = rm[jj].y * vp[jj] + rm[jj].x * vq[jj];
       }
       // next round's players: p -> p - 1 (1 -> P - 1), player 0 fixed (BF:
-      // sinks stay; otherwise an item beyond nitem is never read)
+      // sinks stay; otherwise an item beyond nitem, read but never stored,
+      // keeps offsets inside the P x P entries: oq cycles through P .. (P-1) P)
       const int np = op[jj] < 2 * P ? op[jj] + (P - 2) * P : op[jj] - P;
       const int nq = oq[jj] < 2 * P ? oq[jj] + (P - 2) * P : oq[jj] - P;
       if constexpr (BF) {
