@@ -1159,10 +1159,7 @@ __device__ __forceinline__ void jacobi_eig(double* Gs, double* G2, double* Ws, d
     }
     double c0, s0;
     jacobi_rotation(app, aqq, apq, c0, s0);
-    if (BF)
-      wrot[mr] = make_double2(c0, s0);  // lanes >= NP rewrite their pair's slot with the same value
-    else if (lane < NPr)
-      wrot[lane] = make_double2(c0, s0);
+    wrot[mr] = make_double2(c0, s0);  // lanes >= NPr rewrite their pair's slot with the same value
     wave_sync();
     const double2 ri = wrot[mi], rk = wrot[mk];
     double2 rm[WJ];
