@@ -896,6 +896,15 @@ __device__ __forceinline__ void cholesky_inv_wave(double* Gs, float* Xf, double*
   __syncthreads();
 }
 
+// Maximum over the 64 lanes of a wave, in every lane (as wave_sum_dpp).
+__device__ __forceinline__ float wave_max_dpp(float v) {
+  v = fmaxf(v, __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), 0xB1, 0xF, 0xF, false)));
+  v = fmaxf(v, __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), 0x4E, 0xF, 0xF, false)));
+  v = fmaxf(v, __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), 0x141, 0xF, 0xF, false)));
+  v = fmaxf(v, __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), 0x140, 0xF, 0xF, false)));
+  return max_over_rows(v);
+}
+
 // Sum over the 64 lanes of a wave: DPP quad permutes, row half-mirror and
 // row mirror (every 16-lane row), then permlane32 / permlane16 swaps.
 __device__ __forceinline__ float wave_sum_dpp(float v) {
@@ -1480,14 +1489,32 @@ __device__ __forceinline__ void run_matrix(const RsvdParams& p, const Job& j, in
   }
   __syncthreads();
   // basis
-  for (int e = t; e < j.kp * cols; e += kThreads) {
-    const int i = e / cols, d = e % cols;
-    const float v = i < k ? (float)(L.Zs[i * cols + d] * L.red[i]) : 0.f;
-    if (j.basis_dmajor)
-      j.basis[(long)d * j.kp + i] = (h16)v;
-    else
-      j.basis[(long)i * cols + d] = (h16)v;
-    if (p.vh_out && dbg_index >= 0 && i < k) p.vh_out[(dbg_index * k + i) * cols + d] = v;
+  auto basis_value = [&](int i, int d) __attribute__((always_inline)) {
+    return i < k ? (float)(L.Zs[i * cols + d] * L.red[i]) : 0.f;
+  };
+  const bool dbg_vh = p.vh_out && dbg_index >= 0;
+  if (!dbg_vh && j.kp % 8 == 0 && cols % 8 == 0 && (reinterpret_cast<uintptr_t>(j.basis) & 15) == 0) {
+    // eight consecutive values of the output layout per 16-byte store
+    const int per = (j.basis_dmajor ? j.kp : cols) / 8;
+    const int n_items = (j.basis_dmajor ? cols : j.kp) * per;
+    for (int e = t; e < n_items; e += kThreads) {
+      const int a = e / per, b0 = (e % per) * 8;
+      half8_t h;
+#pragma unroll
+      for (int u = 0; u < 8; ++u)
+        h[u] = (h16)(j.basis_dmajor ? basis_value(b0 + u, a) : basis_value(a, b0 + u));  // (rank, column)
+      *reinterpret_cast<half8_t*>(j.basis + (long)a * (j.basis_dmajor ? j.kp : cols) + b0) = h;
+    }
+  } else {
+    for (int e = t; e < j.kp * cols; e += kThreads) {
+      const int i = e / cols, d = e % cols;
+      const float v = basis_value(i, d);
+      if (j.basis_dmajor)
+        j.basis[(long)d * j.kp + i] = (h16)v;
+      else
+        j.basis[(long)i * cols + d] = (h16)v;
+      if (dbg_vh && i < k) p.vh_out[(dbg_index * k + i) * cols + d] = v;
+    }
   }
   // ---- quantise (spectral_cache.py:481-516 formula); each thread re-reads
   // its own coefficient rows from Ys
@@ -1512,7 +1539,7 @@ __device__ __forceinline__ void run_matrix(const RsvdParams& p, const Job& j, in
   float* fred = (float*)L.red;
   __syncthreads();
   {
-    const float wa = wave_max(fmaxf(am0, am1)), wmn = -wave_max(-mn), wmx = wave_max(mx);
+    const float wa = wave_max_dpp(fmaxf(am0, am1)), wmn = -wave_max_dpp(-mn), wmx = wave_max_dpp(mx);
     if ((t & 63) == 0) {
       fred[t >> 6] = wa;
       fred[4 + (t >> 6)] = wmn;
@@ -1530,7 +1557,7 @@ __device__ __forceinline__ void run_matrix(const RsvdParams& p, const Job& j, in
   float smax = sh;
   if (per_row) {
     __syncthreads();
-    const float ws = wave_max(fmaxf(v0 ? s0 : 0.f, v1 ? s1 : 0.f));
+    const float ws = wave_max_dpp(fmaxf(v0 ? s0 : 0.f, v1 ? s1 : 0.f));
     if ((t & 63) == 0) fred[12 + (t >> 6)] = ws;
     __syncthreads();
     smax = fmaxf(fmaxf(fred[12], fred[13]), fmaxf(fred[14], fred[15]));
@@ -1544,6 +1571,13 @@ __device__ __forceinline__ void run_matrix(const RsvdParams& p, const Job& j, in
       if (v1) j.codes[(long)(t + kThreads) * j.kp + i] = q1;
     }
   };
+  // row-major codes with kp a multiple of 4 and an aligned base: four
+  // codes of a row per dword store
+  const bool pack = !j.coeff_major && j.kp % 4 == 0 && (reinterpret_cast<uintptr_t>(j.codes) & 3) == 0;
+  auto pack4 = [](const int8_t (&q)[4]) __attribute__((always_inline)) {
+    return (uint32_t)(uint8_t)q[0] | ((uint32_t)(uint8_t)q[1] << 8) | ((uint32_t)(uint8_t)q[2] << 16) |
+           ((uint32_t)(uint8_t)q[3] << 24);
+  };
 #pragma unroll
   for (int i = 0; i < RM; i += 4) {
     if (i < j.kp) {
@@ -1551,20 +1585,33 @@ __device__ __forceinline__ void run_matrix(const RsvdParams& p, const Job& j, in
       const float4 a4 = v0 ? *reinterpret_cast<const float4*>(L.Ys + t * RM + i) : zero4;
       const float4 b4 = v1 ? *reinterpret_cast<const float4*>(L.Ys + (t + kThreads) * RM + i) : zero4;
       const float ca[4] = {a4.x, a4.y, a4.z, a4.w}, cb[4] = {b4.x, b4.y, b4.z, b4.w};
+      int8_t qa[4], qb[4];
 #pragma unroll
       for (int u = 0; u < 4; ++u) {
-        if (i + u < j.kp) {
-          int8_t q0 = 0, q1 = 0;
-          if (i + u < k) {
-            q0 = (int8_t)(int)rintf(ca[u] / s0);  // IEEE division, ties to even
-            q1 = (int8_t)(int)rintf(cb[u] / s1);
-          }
-          put(i + u, q0, q1);
+        qa[u] = qb[u] = 0;
+        if (i + u < k) {
+          qa[u] = (int8_t)(int)rintf(ca[u] / s0);  // IEEE division, ties to even
+          qb[u] = (int8_t)(int)rintf(cb[u] / s1);
         }
+      }
+      if (pack) {
+        if (v0) *reinterpret_cast<uint32_t*>(j.codes + (long)t * j.kp + i) = pack4(qa);
+        if (v1) *reinterpret_cast<uint32_t*>(j.codes + (long)(t + kThreads) * j.kp + i) = pack4(qb);
+      } else {
+#pragma unroll
+        for (int u = 0; u < 4; ++u)
+          if (i + u < j.kp) put(i + u, qa[u], qb[u]);
       }
     }
   }
-  for (int i = RM; i < j.kp; ++i) put(i, 0, 0);
+  if (pack) {
+    for (int i = RM; i < j.kp; i += 4) {
+      if (v0) *reinterpret_cast<uint32_t*>(j.codes + (long)t * j.kp + i) = 0u;
+      if (v1) *reinterpret_cast<uint32_t*>(j.codes + (long)(t + kThreads) * j.kp + i) = 0u;
+    }
+  } else {
+    for (int i = RM; i < j.kp; ++i) put(i, 0, 0);
+  }
   if (per_row) {
     if (v0) j.scales[t] = s0;
     if (v1) j.scales[t + kThreads] = s1;
