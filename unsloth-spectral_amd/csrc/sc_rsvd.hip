@@ -1581,18 +1581,16 @@ __device__ __forceinline__ void run_matrix(const RsvdParams& p, const Job& j, in
 #pragma unroll
   for (int i = 0; i < RM; i += 4) {
     if (i < j.kp) {
-      const float4 zero4 = make_float4(0.f, 0.f, 0.f, 0.f);
-      const float4 a4 = v0 ? *reinterpret_cast<const float4*>(L.Ys + t * RM + i) : zero4;
-      const float4 b4 = v1 ? *reinterpret_cast<const float4*>(L.Ys + (t + kThreads) * RM + i) : zero4;
+      // rows t and t + kThreads < kMaxRows: in bounds (rows past `rows`
+      // are never stored); columns >= k hold 0, whose code is 0
+      const float4 a4 = *reinterpret_cast<const float4*>(L.Ys + t * RM + i);
+      const float4 b4 = *reinterpret_cast<const float4*>(L.Ys + (t + kThreads) * RM + i);
       const float ca[4] = {a4.x, a4.y, a4.z, a4.w}, cb[4] = {b4.x, b4.y, b4.z, b4.w};
       int8_t qa[4], qb[4];
 #pragma unroll
       for (int u = 0; u < 4; ++u) {
-        qa[u] = qb[u] = 0;
-        if (i + u < k) {
-          qa[u] = (int8_t)(int)rintf(ca[u] / s0);  // IEEE division, ties to even
-          qb[u] = (int8_t)(int)rintf(cb[u] / s1);
-        }
+        qa[u] = (int8_t)(int)rintf(ca[u] / s0);  // IEEE division, ties to even
+        qb[u] = (int8_t)(int)rintf(cb[u] / s1);
       }
       if (pack) {
         if (v0) *reinterpret_cast<uint32_t*>(j.codes + (long)t * j.kp + i) = pack4(qa);
