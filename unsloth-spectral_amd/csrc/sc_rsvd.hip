@@ -495,7 +495,10 @@ template <int RM>
 __device__ __forceinline__ void gemm_cols_mfma_ct(const Job& j, int rows, const float* Ys, float* Zs, h16* stage) {
   Ys = lds_base(Ys);
   Zs = lds_base(Zs);
-  stage = lds_base(stage);
+  // two staging buffers: `stage` and the output Zs, which is written only
+  // after the last tile
+  static_assert(sizeof(float) * 128 * RM >= sizeof(h16) * kColTile * (128 + 8), "a staged tile fits in Zs");
+  h16* const stg[2] = {lds_base(stage), lds_base(reinterpret_cast<h16*>(Zs))};
   constexpr int CT = (RM + 15) / 16;
   static_assert(CT == 2 || CT == 3, "two or three column tiles of Ys");
   constexpr int NDT = CT == 2 ? 4 : 8;  // d tiles per wave
@@ -515,19 +518,22 @@ __device__ __forceinline__ void gemm_cols_mfma_ct(const Job& j, int rows, const 
     x0 = *reinterpret_cast<const uint4*>(row_ptr(j, k0 + c0 / cpr, cols) + (c0 % cpr) * 16);
     x1 = *reinterpret_cast<const uint4*>(row_ptr(j, k0 + c1 / cpr, cols) + (c1 % cpr) * 16);
   };
-  auto put = [&](const uint4& x0, const uint4& x1) __attribute__((always_inline)) {
+  auto put = [&](h16* stage, const uint4& x0, const uint4& x1) __attribute__((always_inline)) {
     *reinterpret_cast<uint4*>(stage + (c0 / cpr) * pitch + (c0 % cpr) * 8) = x0;
     *reinterpret_cast<uint4*>(stage + (c1 / cpr) * pitch + (c1 % cpr) * 8) = x1;
   };
   fetch(0, nx0, nx1);
   if (kColTile < rows) fetch(kColTile, nn0, nn1);
-  put(nx0, nx1);
+  put(stg[0], nx0, nx1);
   __syncthreads();
-  // step(k0, a, b): b holds tile k0 + kColTile (in flight), a is free and
-  // receives tile k0 + 2 kColTile; two steps per iteration swap the roles
-  // (no register copies, which would wait for the loads)
-  auto step = [&](int k0, uint4& a0, uint4& a1, const uint4& b0, const uint4& b1) __attribute__((always_inline)) {
-    const bool more = k0 + kColTile < rows;
+  // step(k0, a, b) with tile k0 staged in stg[sb]: b holds tile k0 +
+  // kColTile (in flight), a is free and receives tile k0 + 2 kColTile.
+  // After the tile's products, b goes to the other buffer (last read by the
+  // previous tile, before the barrier that ended it): one barrier per tile.
+  // Two steps per iteration swap the register roles (no register copies,
+  // which would wait for the loads).
+  auto step = [&](int k0, int sb, uint4& a0, uint4& a1, const uint4& b0, const uint4& b1) __attribute__((always_inline)) {
+    const h16* stage = stg[sb];
     if (k0 + 2 * kColTile < rows) fetch(k0 + 2 * kColTile, a0, a1);
     if (busy) {
       half8_t a[NDT];
@@ -554,15 +560,12 @@ __device__ __forceinline__ void gemm_cols_mfma_ct(const Job& j, int rows, const 
         acc[dt] = __builtin_amdgcn_mfma_f32_16x16x32_f16(a[dt], bl, acc[dt], 0, 0, 0);
       }
     }
-    __syncthreads();  // every wave is done with this tile
-    if (more) {
-      put(b0, b1);
-      __syncthreads();
-    }
+    if (k0 + kColTile < rows) put(stg[sb ^ 1], b0, b1);
+    __syncthreads();  // this tile's reads and the next tile's stores are done
   };
   for (int k0 = 0; k0 < rows; k0 += 2 * kColTile) {
-    step(k0, nx0, nx1, nn0, nn1);
-    if (k0 + kColTile < rows) step(k0 + kColTile, nn0, nn1, nx0, nx1);
+    step(k0, 0, nx0, nx1, nn0, nn1);
+    if (k0 + kColTile < rows) step(k0 + kColTile, 1, nn0, nn1, nx0, nx1);
   }
   if (busy && c < RM)
 #pragma unroll
