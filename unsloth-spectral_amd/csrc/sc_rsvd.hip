@@ -1153,6 +1153,30 @@ __device__ __forceinline__ void jacobi_eig(double* Gs, double* G2, double* Ws, d
     op[jj] = BF && !iv[jj] ? sink : m * P + c;  // BF: items beyond nitem read and write the sink
     oq[jj] = BF && !iv[jj] ? sink : (P - 1 - m) * P + c;
   }
+  // PIPE (RM = 40): the eigenvector update of a round is applied one round
+  // later (W never feeds the rotations), off the critical path of the next
+  // round's rotations: pr/pop/poq hold the pending rotation and offsets of
+  // each item, initially the identity at the first round's offsets.  At
+  // RM = 24 (fewer items per thread) the update stays in its own round.
+  constexpr bool PIPE = RM > 24;
+  double2 pr[WJ];
+  int pop[WJ], poq[WJ];
+#pragma unroll
+  for (int jj = 0; jj < WJ; ++jj) {
+    pr[jj] = make_double2(1.0, 0.0);
+    pop[jj] = op[jj];
+    poq[jj] = oq[jj];
+  }
+  auto w_update = [&](const double2 (&rot)[WJ], const int (&o1)[WJ], const int (&o2)[WJ], const double (&vp)[WJ],
+                      const double (&vq)[WJ]) __attribute__((always_inline)) {
+#pragma unroll
+    for (int jj = 0; jj < WJ; ++jj) {
+      if (BF || iv[jj]) {
+        Ws[o1[jj]] = rot[jj].x * vp[jj] - rot[jj].y * vq[jj];
+        Ws[o2[jj]] = rot[jj].y * vp[jj] + rot[jj].x * vq[jj];
+      }
+    }
+  };
   double* cur = G2;
   double* nxt = Gs;
   auto round = [&](const double* gc, double* gn) __attribute__((always_inline)) {
@@ -1163,11 +1187,11 @@ __device__ __forceinline__ void jacobi_eig(double* Gs, double* G2, double* Ws, d
     // unused stores are skipped by lane masks.
     const double app = gc[o_pp], aqq = gc[o_qq], apq = gc[o_pq];
     const double a00 = gc[r00], a01 = gc[r01], a10 = gc[r10], a11 = gc[r11];
-    double vp[WJ], vq[WJ];
+    double vp[WJ], vq[WJ];  // PIPE: the pending update's entries; else this round's
 #pragma unroll
     for (int jj = 0; jj < WJ; ++jj) {
-      vp[jj] = Ws[op[jj]];
-      vq[jj] = Ws[oq[jj]];
+      vp[jj] = Ws[PIPE ? pop[jj] : op[jj]];
+      vq[jj] = Ws[PIPE ? poq[jj] : oq[jj]];
     }
     double c0, s0;
     jacobi_rotation(app, aqq, apq, c0, s0);
@@ -1190,12 +1214,19 @@ __device__ __forceinline__ void jacobi_eig(double* Gs, double* G2, double* Ws, d
         if (BF || mi != mk) gn[w10] = n10;  // a diagonal block's (y, x) is its (x, y) (BF: w10 is the sink)
       }
     }
+    if constexpr (PIPE) {
+      w_update(pr, pop, poq, vp, vq);  // the previous round's
+#pragma unroll
+      for (int jj = 0; jj < WJ; ++jj) {
+        pr[jj] = rm[jj];  // this round's, applied next round
+        pop[jj] = op[jj];
+        poq[jj] = oq[jj];
+      }
+    } else {
+      w_update(rm, op, oq, vp, vq);
+    }
 #pragma unroll
     for (int jj = 0; jj < WJ; ++jj) {
-      if (BF || iv[jj]) {
-        Ws[op[jj]] = rm[jj].x * vp[jj] - rm[jj].y * vq[jj];
-        Ws[oq[jj]] = rm[jj].y * vp[jj] + rm[jj].x * vq[jj];
-      }
       // next round's players: p -> p - 1 (1 -> P - 1), player 0 fixed (BF:
       // sinks stay; otherwise an item beyond nitem, read but never stored,
       // keeps offsets inside the P x P entries: oq cycles through P .. (P-1) P)
@@ -1250,6 +1281,15 @@ __device__ __forceinline__ void jacobi_eig(double* Gs, double* G2, double* Ws, d
       cur = B;
       nxt = A;
     }
+  }
+  if constexpr (PIPE) {  // the last round's eigenvector update
+    double vp[WJ], vq[WJ];
+#pragma unroll
+    for (int jj = 0; jj < WJ; ++jj) {
+      vp[jj] = Ws[pop[jj]];
+      vq[jj] = Ws[poq[jj]];
+    }
+    w_update(pr, pop, poq, vp, vq);
   }
   // eigenvalues to the diagonal of Gs (stride RM); cur may overlap Gs
   const double ev = t < P ? cur[t * P + t] : 0.0;
