@@ -320,14 +320,14 @@ __device__ __forceinline__ void gemm_rows_mfma(const Job& j, int rows, int cols,
 #pragma unroll
     for (int ct = 0; ct < CT; ++ct) {
       const int c = 16 * ct + n;
+      const bool in = s < KS && c < RM;  // s < KS is wave-uniform
+      float v[8];
 #pragma unroll
-      for (int e = 0; e < 8; ++e) {
-        const float v = (s < KS && c < RM) ? Zs[(32 * s + 8 * g + e) * RM + c] : 0.f;
-        h16 hi, lo;
-        split16(v, hi, lo);
-        bh[s][ct][e] = hi;
-        bl[s][ct][e] = lo;
+      for (int e = 0; e < 8; ++e) {  // clamped (in-bounds) loads and a select: no exec-masked loads
+        const float z = Zs[(32 * min(s, KS - 1) + 8 * g + e) * RM + min(c, RM - 1)];
+        v[e] = in ? z : 0.f;
       }
+      split16x8(v, bh[s][ct], bl[s][ct]);
     }
   if (rows == kMaxRows && cols == 128) {
     // the block geometry: a wave's 8 row tiles in two batches of 4, each
