@@ -306,9 +306,27 @@ __device__ __forceinline__ void split16x8(const float (&v)[8], half8_t& hi, half
   }
 }
 
+// One batch of a wave's row tiles of a 512x128 block for gemm_rows_mfma:
+// tiles w + 4 (b0 + i), i < kRowBatch, as MFMA A operands.
+constexpr int kRowBatch = 4;
+struct RowBatch {
+  half8_t a[kRowBatch][4];
+};
+__device__ __forceinline__ void load_row_batch(const Job& j, int b0, RowBatch& rb) {
+  constexpr int NW = kThreads / 64;
+  const int lane = threadIdx.x & 63, g = lane >> 4, n = lane & 15, w = threadIdx.x >> 6;
+#pragma unroll
+  for (int i = 0; i < kRowBatch; ++i) {
+    const h16* rp = reinterpret_cast<const h16*>(row_ptr(j, 16 * (w + NW * (b0 + i)) + n, 128));
+#pragma unroll
+    for (int s = 0; s < 4; ++s) rb.a[i][s] = *reinterpret_cast<const half8_t*>(rp + 32 * s + 8 * g);
+  }
+}
+
 // Ys[rows][RM] = M[rows][cols] Zs[cols][RM]; wave w takes row tiles w, w+4, ...
 template <int RM>
-__device__ __forceinline__ void gemm_rows_mfma(const Job& j, int rows, int cols, const float* Zs, float* Ys) {
+__device__ __forceinline__ void gemm_rows_mfma(const Job& j, int rows, int cols, const float* Zs, float* Ys,
+                                               const RowBatch* pre = nullptr) {
   Zs = lds_base(Zs);
   Ys = lds_base(Ys);
   constexpr int CT = (RM + 15) / 16;
@@ -331,17 +349,10 @@ __device__ __forceinline__ void gemm_rows_mfma(const Job& j, int rows, int cols,
     }
   if (rows == kMaxRows && cols == 128) {
     // the block geometry: a wave's 8 row tiles in two batches of 4, each
-    // batch's loads issued together (two memory round trips, not eight)
-    constexpr int NW = kThreads / 64, BT = 4;
-#pragma unroll 1
-    for (int b0 = 0; b0 < kMaxRows / 16 / NW; b0 += BT) {
-      half8_t a[BT][4];
-#pragma unroll
-      for (int i = 0; i < BT; ++i) {
-        const h16* rp = reinterpret_cast<const h16*>(row_ptr(j, 16 * (w + NW * (b0 + i)) + n, cols));
-#pragma unroll
-        for (int s = 0; s < 4; ++s) a[i][s] = *reinterpret_cast<const half8_t*>(rp + 32 * s + 8 * g);
-      }
+    // batch's loads issued together (two memory round trips, not eight);
+    // `pre` (when given) is the first batch, loaded by the caller earlier
+    constexpr int NW = kThreads / 64, BT = kRowBatch;
+    auto batch = [&](int b0, const RowBatch& rb) __attribute__((always_inline)) {
 #pragma unroll
       for (int i = 0; i < BT; ++i) {
         const int rt = w + NW * (b0 + i);
@@ -350,8 +361,8 @@ __device__ __forceinline__ void gemm_rows_mfma(const Job& j, int rows, int cols,
           float4_t acc = (float4_t)0.f;
 #pragma unroll
           for (int s = 0; s < 4; ++s) {
-            acc = __builtin_amdgcn_mfma_f32_16x16x32_f16(a[i][s], bh[s][ct], acc, 0, 0, 0);
-            acc = __builtin_amdgcn_mfma_f32_16x16x32_f16(a[i][s], bl[s][ct], acc, 0, 0, 0);
+            acc = __builtin_amdgcn_mfma_f32_16x16x32_f16(rb.a[i][s], bh[s][ct], acc, 0, 0, 0);
+            acc = __builtin_amdgcn_mfma_f32_16x16x32_f16(rb.a[i][s], bl[s][ct], acc, 0, 0, 0);
           }
           const int c = 16 * ct + n;
           if (c < RM)
@@ -359,6 +370,17 @@ __device__ __forceinline__ void gemm_rows_mfma(const Job& j, int rows, int cols,
             for (int jj = 0; jj < 4; ++jj) Ys[(16 * rt + 4 * g + jj) * RM + c] = acc[jj];
         }
       }
+    };
+    int b0 = 0;
+    if (pre) {
+      batch(0, *pre);
+      b0 = BT;
+    }
+#pragma unroll 1
+    for (; b0 < kMaxRows / 16 / NW; b0 += BT) {
+      RowBatch rb;
+      load_row_batch(j, b0, rb);
+      batch(b0, rb);
     }
     return;
   }
@@ -1304,6 +1326,12 @@ __device__ __forceinline__ void run_matrix(const RsvdParams& p, const Job& j, in
   const int t = threadIdx.x;
   const int r = j.r, k = j.k;
   const int P = r + (r & 1);  // Jacobi players: the eigenvectors are rows of Ws with stride P
+  const bool mf = j.dtype == SC_DTYPE_F16 && !j.rw;  // MFMA products (fp16 input, unweighted); else fp32 VALU
+  // the first M Z's first row batch, requested before the sketch is drawn
+  // (the block's first reads from HBM overlap the sketch generation)
+  const bool pre = mf && rows == kMaxRows && cols == 128;
+  RowBatch rb0;
+  if (pre) load_row_batch(j, 0, rb0);
   // ---- sketch
   for (int e = t; e < 128 * RM; e += kThreads) L.Zs[e] = 0.f;
   __syncthreads();
@@ -1321,7 +1349,6 @@ __device__ __forceinline__ void run_matrix(const RsvdParams& p, const Job& j, in
   if (p.omega_out && dbg_index >= 0)
     for (int e = t; e < cols * r; e += kThreads) p.omega_out[dbg_index * cols * r + e] = L.Zs[(e / r) * RM + e % r];
 
-  const bool mf = j.dtype == SC_DTYPE_F16 && !j.rw;  // MFMA products (fp16 input, unweighted); else fp32 VALU
   auto mul_m = [&]() __attribute__((always_inline)) {  // Ys = M Zs
     if (mf) {
       gemm_rows_mfma<RM>(j, rows, cols, L.Zs, L.Ys);
@@ -1348,7 +1375,10 @@ __device__ __forceinline__ void run_matrix(const RsvdParams& p, const Job& j, in
       apply_rinv<RM>(L.Ys, rows, L.Wf);
     }
   };
-  mul_m();
+  if (pre)
+    gemm_rows_mfma<RM>(j, rows, cols, L.Zs, L.Ys, &rb0);
+  else
+    mul_m();
   if (n_iter > 0) {
     // The sketch is only scaled (unit columns; the span is unchanged): that
     // bounds M^T Y like an orthonormal Y would, so the fp16 hi/lo split of
