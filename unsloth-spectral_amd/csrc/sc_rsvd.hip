@@ -5,8 +5,8 @@
 //
 // Per matrix M [rows <= 512][cols in {64,128}] (fp16/bf16/fp32, exact in fp32):
 //   Z   <- Omega                                   (given, or Philox4x32-10)
-//   Y   <- M Z ;  Y <- orth(Y)                      \  n_iter times:
-//   Z   <- M^T Y ; Y <- M Z ; Y <- orth(Y)          /  same subspace as the
+//   Y   <- M Z, columns scaled to unit norm         (n_iter = 0: Y <- orth(Y), two passes)
+//   Z   <- M^T Y ; Y <- M Z ; Y <- orth(Y)          n_iter times: same subspace as the
 //                                                     reference's (M M^T)^q M Omega
 //   Bp^T <- M^T Y                                   (Bp = Q^T M, r x cols)
 //   eig(Bp Bp^T) = W diag(lambda) W^T               (fp64 parallel Jacobi)
@@ -17,9 +17,10 @@
 // hi + lo parts, so the result keeps fp32 accuracy) and the Gram matrices on
 // the fp64 MFMA; other input types use fp32 VALU products.  orth() is
 // CholeskyQR (one pass between iterations, two for the final Q): fp64
-// Cholesky by one wave with its rows in registers, then a forward solve of
-// every row of Y against R.  Columns whose Cholesky pivot vanishes are
-// zeroed, so rank-deficient blocks (zeros, repeated rows) stay finite.
+// Cholesky by one wave with its rows in registers, R^{-1} by all four waves,
+// then Y <- Y R^{-1} row by row in fp32.  Columns whose Cholesky pivot
+// vanishes are zeroed, so rank-deficient blocks (zeros, repeated rows) stay
+// finite.
 #include <math.h>
 
 #include <utility>
@@ -1102,15 +1103,17 @@ __device__ __forceinline__ void jacobi_rotation(double app, double aqq, double a
 // reads, then:
 //   * each wave computes the rotations (c, s) of all pairs, lane l taking
 //     pair l % NP (every wave computes the same values from the same
-//     entries); lanes l < NP store them in the wave's own slot of rot and the
-//     wave's lanes read back those they need (no barrier);
+//     entries); every lane stores its pair's rotation in the wave's own slot
+//     of rot (lanes of one pair store the same value) and the wave's lanes
+//     read back those they need (no barrier);
 //   * thread i < NB rotates the 2x2 block (pair mi, pair mk), mi <= mk, from
 //     both sides (G <- J^T G J) into the other buffer (a diagonal block has
 //     three distinct entries);
 //   * the (pair m, row c) items of the eigenvector update, m * P + c = t,
-//     t + kThreads, ..., rotate entries (players of m, c) of Ws in place;
-//     the players of a position move by one per round, so the two LDS
-//     offsets of an item are updated by one compare and select each.
+//     t + kThreads, ..., rotate entries (players of m, c) of Ws in place
+//     (at RM = 40 one round later, off the rotation chain); the players of a
+//     position move by one per round, so the two LDS offsets of an item are
+//     updated by one compare and select each.
 // Stops at a sweep boundary when the off-diagonal mass is <= 1e-10 of the
 // diagonal mass (the off-diagonal norm below 1e-5 of the diagonal's): the
 // eigenvectors then mix the retained and the dropped directions by ~1e-5,
