@@ -1473,13 +1473,19 @@ __device__ __forceinline__ void run_matrix(const RsvdParams& p, const Job& j, in
         }
       }
     } else {
-      // one column per step (fewer registers in flight at RM = 40)
+      // one column per step (fewer registers in flight at RM = 40); one
+      // base register per array, so a step's Wf row loads are issued
+      // together with immediate offsets
+      const float* ya = lds_base(L.Ys) + t * RM;
+      const float* wf = lds_base(L.Wf);
 #pragma unroll 1
       for (int c = 0; c < r; ++c) {
-        const float q0 = v0 ? L.Ys[t * RM + c] : 0.f, q1 = v1 ? L.Ys[(t + kThreads) * RM + c] : 0.f;
+        const float a = ya[c], b = ya[kThreads * RM + c];  // rows t, t + kThreads < kMaxRows: in bounds
+        const float q0 = v0 ? a : 0.f, q1 = v1 ? b : 0.f;
+        const float* wr = wf + c * RM;
 #pragma unroll
         for (int i = 0; i < RM; i += 4) {  // Wf[c][i] = 0 for i >= k: those accumulators stay 0
-          const float4 w = *reinterpret_cast<const float4*>(L.Wf + c * RM + i);
+          const float4 w = *reinterpret_cast<const float4*>(wr + i);
           cf0[i] = fmaf(q0, w.x, cf0[i]);
           cf0[i + 1] = fmaf(q0, w.y, cf0[i + 1]);
           cf0[i + 2] = fmaf(q0, w.z, cf0[i + 2]);
