@@ -1411,16 +1411,27 @@ __device__ __forceinline__ void run_matrix(const RsvdParams& p, const Job& j, in
   gram_mfma<RM>(L.Zs, cols, r, L.Gs);  // Bp Bp^T
   __syncthreads();
   jacobi_eig<RM>(L.Gs, L.G2, L.Ws, L.red, reinterpret_cast<double2*>(L.Wf), r);  // Wf: dead here
+  // The epilogue's LDS arrays through opaque bases (one base register per
+  // array plus immediate offsets; several lie past the 64 KB reach of an
+  // immediate at RM = 40).
+  Lds<RM> E = L;
+  E.Gs = lds_base(L.Gs);
+  E.Ws = lds_base(L.Ws);
+  E.Ys = lds_base(L.Ys);
+  E.Zs = lds_base(L.Zs);
+  E.Wf = lds_base(L.Wf);
+  E.red = lds_base(L.red);
+  E.ord = lds_base(L.ord);
   // ---- eigenvalues in descending order: lane c takes rank = #{larger, or equal with lower index}
   if (t < r) {
-    const double lc = L.Gs[t * RM + t];
+    const double lc = E.Gs[t * RM + t];
     int rank = 0;
 #pragma unroll
     for (int b2 = 0; b2 < RM; ++b2) {  // every load in flight at once; b2 >= r masked
-      const double lb = L.Gs[b2 * RM + b2];
+      const double lb = E.Gs[b2 * RM + b2];
       rank += b2 < r && ((lb > lc) || (lb == lc && b2 < t));
     }
-    L.ord[rank] = t;
+    E.ord[rank] = t;
   }
   __syncthreads();
   // Wf[c][i] = W[c][ord_i] * S_i  (c < r, i < k; 0 elsewhere)
@@ -1428,10 +1439,10 @@ __device__ __forceinline__ void run_matrix(const RsvdParams& p, const Job& j, in
     const int c = e / RM, i = e % RM;
     float v = 0.f;
     if (c < r && i < k) {
-      const int oi = L.ord[i];
-      v = (float)(L.Ws[oi * P + c] * sqrt(fmax(L.Gs[oi * RM + oi], 0.0)));
+      const int oi = E.ord[i];
+      v = (float)(E.Ws[oi * P + c] * sqrt(fmax(E.Gs[oi * RM + oi], 0.0)));
     }
-    L.Wf[e] = v;
+    E.Wf[e] = v;
   }
   __syncthreads();
   // ---- coefficients, in place over the Q rows of Ys: Ys[row][i] =
@@ -1447,8 +1458,8 @@ __device__ __forceinline__ void run_matrix(const RsvdParams& p, const Job& j, in
     if constexpr (RM <= 24) {
       // four columns per step: two float4 row loads and 4 x RM / 4 Wf loads
       // in flight together
-      const float* ya = lds_base(L.Ys) + t * RM;
-      const float* wf = lds_base(L.Wf);
+      const float* ya = E.Ys + t * RM;
+      const float* wf = E.Wf;
 #pragma unroll 1
       for (int c4 = 0; c4 < RM; c4 += 4) {
         const float4 a4 = *reinterpret_cast<const float4*>(ya + c4);  // rows t, t + kThreads < kMaxRows: in bounds
@@ -1476,8 +1487,8 @@ __device__ __forceinline__ void run_matrix(const RsvdParams& p, const Job& j, in
       // one column per step (fewer registers in flight at RM = 40); one
       // base register per array, so a step's Wf row loads are issued
       // together with immediate offsets
-      const float* ya = lds_base(L.Ys) + t * RM;
-      const float* wf = lds_base(L.Wf);
+      const float* ya = E.Ys + t * RM;
+      const float* wf = E.Wf;
 #pragma unroll 1
       for (int c = 0; c < r; ++c) {
         const float a = ya[c], b = ya[kThreads * RM + c];  // rows t, t + kThreads < kMaxRows: in bounds
@@ -1509,16 +1520,16 @@ __device__ __forceinline__ void run_matrix(const RsvdParams& p, const Job& j, in
     // Wf[c][i] = 0 for i >= k, so cf[i] = 0 there: whole rows are stored
 #pragma unroll
     for (int i = 0; i < RM; i += 4) {
-      if (v0) *reinterpret_cast<float4*>(L.Ys + t * RM + i) = make_float4(cf0[i], cf0[i + 1], cf0[i + 2], cf0[i + 3]);
+      if (v0) *reinterpret_cast<float4*>(E.Ys + t * RM + i) = make_float4(cf0[i], cf0[i + 1], cf0[i + 2], cf0[i + 3]);
       if (v1)
-        *reinterpret_cast<float4*>(L.Ys + (t + kThreads) * RM + i) =
+        *reinterpret_cast<float4*>(E.Ys + (t + kThreads) * RM + i) =
             make_float4(cf1[i], cf1[i + 1], cf1[i + 2], cf1[i + 3]);
     }
   }
   if (p.coeffs_out && dbg_index >= 0) {
     for (int i = 0; i < k; ++i) {
-      if (v0) p.coeffs_out[(dbg_index * rows + t) * k + i] = L.Ys[t * RM + i];
-      if (v1) p.coeffs_out[(dbg_index * rows + t + kThreads) * k + i] = L.Ys[(t + kThreads) * RM + i];
+      if (v0) p.coeffs_out[(dbg_index * rows + t) * k + i] = E.Ys[t * RM + i];
+      if (v1) p.coeffs_out[(dbg_index * rows + t + kThreads) * k + i] = E.Ys[(t + kThreads) * RM + i];
     }
   }
   // Vh (unnormalised), in place over Bp^T in Zs, as [k][cols]:
@@ -1531,7 +1542,7 @@ __device__ __forceinline__ void run_matrix(const RsvdParams& p, const Job& j, in
     float z[RM];
 #pragma unroll
     for (int c = 0; c < RM; c += 4) {
-      const float4 z4 = *reinterpret_cast<const float4*>(L.Zs + d * RM + c);
+      const float4 z4 = *reinterpret_cast<const float4*>(E.Zs + d * RM + c);
       z[c] = z4.x;
       z[c + 1] = z4.y;
       z[c + 2] = z4.z;
@@ -1542,7 +1553,7 @@ __device__ __forceinline__ void run_matrix(const RsvdParams& p, const Job& j, in
     for (int i = t / cols; i < k; i += istep) {
       // whole rows of RM entries, no branches: z[c] = 0 for c >= r (the
       // columns of Q beyond r are zero) and Ws is zero beyond P x P
-      const double* wr = L.Ws + L.ord[i] * P;
+      const double* wr = E.Ws + E.ord[i] * P;
       double a0 = 0.0, a1 = 0.0;
 #pragma unroll
       for (int c = 0; c < RM; c += 2) {
@@ -1550,29 +1561,29 @@ __device__ __forceinline__ void run_matrix(const RsvdParams& p, const Job& j, in
         a0 = fma(w2.x, (double)z[c], a0);
         a1 = fma(w2.y, (double)z[c + 1], a1);
       }
-      L.Zs[i * cols + d] = (float)(a0 + a1);
+      E.Zs[i * cols + d] = (float)(a0 + a1);
     }
   }
   __syncthreads();
   for (int i = t >> 6; i < k; i += kThreads / 64) {  // row norms -> 1/norm (0 for vanished rows), one wave per row
     double nn = 0.0;
     for (int d = t & 63; d < cols; d += 64) {
-      const double v = L.Zs[i * cols + d];
+      const double v = E.Zs[i * cols + d];
       nn += v * v;
     }
     nn = wave_reduce_d(nn, [](double a, double b) __attribute__((always_inline)) { return a + b; });
     if ((t & 63) == 0) {
-      L.red[i] = nn > 0.0 ? 1.0 / sqrt(nn) : 0.0;
+      E.red[i] = nn > 0.0 ? 1.0 / sqrt(nn) : 0.0;
       if (p.svals_out && dbg_index >= 0) {
-        const int oi = L.ord[i];
-        p.svals_out[dbg_index * k + i] = (float)sqrt(fmax(L.Gs[oi * RM + oi], 0.0));
+        const int oi = E.ord[i];
+        p.svals_out[dbg_index * k + i] = (float)sqrt(fmax(E.Gs[oi * RM + oi], 0.0));
       }
     }
   }
   __syncthreads();
   // basis
   auto basis_value = [&](int i, int d) __attribute__((always_inline)) {
-    return i < k ? (float)(L.Zs[i * cols + d] * L.red[i]) : 0.f;
+    return i < k ? (float)(E.Zs[i * cols + d] * E.red[i]) : 0.f;
   };
   const bool dbg_vh = p.vh_out && dbg_index >= 0;
   if (!dbg_vh && j.kp % 8 == 0 && cols % 8 == 0 && (reinterpret_cast<uintptr_t>(j.basis) & 15) == 0) {
@@ -1604,7 +1615,7 @@ __device__ __forceinline__ void run_matrix(const RsvdParams& p, const Job& j, in
   auto row_stats = [&](int row, float& am) __attribute__((always_inline)) {
 #pragma unroll
     for (int i = 0; i < RM; i += 4) {  // columns >= k hold 0: masked by selects, no branches
-      const float4 c4 = *reinterpret_cast<const float4*>(L.Ys + row * RM + i);
+      const float4 c4 = *reinterpret_cast<const float4*>(E.Ys + row * RM + i);
       const float cv[4] = {c4.x, c4.y, c4.z, c4.w};
 #pragma unroll
       for (int u = 0; u < 4; ++u) {
@@ -1618,7 +1629,7 @@ __device__ __forceinline__ void run_matrix(const RsvdParams& p, const Job& j, in
   if (v0) row_stats(t, am0);
   if (v1) row_stats(t + kThreads, am1);
   // block reductions: absmax, min, max
-  float* fred = (float*)L.red;
+  float* fred = (float*)E.red;
   __syncthreads();
   {
     const float wa = wave_max_dpp(fmaxf(am0, am1)), wmn = -wave_max_dpp(-mn), wmx = wave_max_dpp(mx);
@@ -1665,8 +1676,8 @@ __device__ __forceinline__ void run_matrix(const RsvdParams& p, const Job& j, in
     if (i < j.kp) {
       // rows t and t + kThreads < kMaxRows: in bounds (rows past `rows`
       // are never stored); columns >= k hold 0, whose code is 0
-      const float4 a4 = *reinterpret_cast<const float4*>(L.Ys + t * RM + i);
-      const float4 b4 = *reinterpret_cast<const float4*>(L.Ys + (t + kThreads) * RM + i);
+      const float4 a4 = *reinterpret_cast<const float4*>(E.Ys + t * RM + i);
+      const float4 b4 = *reinterpret_cast<const float4*>(E.Ys + (t + kThreads) * RM + i);
       const float ca[4] = {a4.x, a4.y, a4.z, a4.w}, cb[4] = {b4.x, b4.y, b4.z, b4.w};
       int8_t qa[4], qb[4];
 #pragma unroll
