@@ -1267,16 +1267,27 @@ __device__ __forceinline__ void jacobi_eig(double* Gs, double* G2, double* Ws, d
     }
     __syncthreads();
   };
+  // stopping test: which of this thread's entries t, t + kThreads, ... are
+  // diagonal / upper (formed once, no division per sweep)
+  constexpr int KE = (RM * RM + kThreads - 1) / kThreads;
+  uint32_t dmask = 0, umask = 0;
+#pragma unroll
+  for (int ke = 0; ke < KE; ++ke) {
+    const int e = t + kThreads * ke;
+    if (e < P * P) {
+      const int i = e / P, k = e % P;
+      dmask |= (i == k ? 1u : 0u) << ke;
+      umask |= (i < k ? 1u : 0u) << ke;
+    }
+  }
   __syncthreads();
   for (int sweep = 0; sweep < 30; ++sweep) {
     double off = 0.0, dia = 0.0;
-    for (int e = t; e < P * P; e += kThreads) {
-      const int i = e / P, k = e % P;
-      const double v = cur[e];
-      if (i == k)
-        dia += v * v;
-      else if (i < k)
-        off += 2.0 * (v * v);
+#pragma unroll
+    for (int ke = 0; ke < KE; ++ke) {
+      const double v = cur[min(t + kThreads * ke, P * P - 1)];
+      dia += ((dmask >> ke) & 1u) ? v * v : 0.0;
+      off += ((umask >> ke) & 1u) ? 2.0 * (v * v) : 0.0;
     }
     auto add = [](double a, double b) __attribute__((always_inline)) { return a + b; };
     off = wave_reduce_d(off, add);
