@@ -283,13 +283,9 @@ __device__ __forceinline__ void gemm_cols(const Job& j, int rows, int cols, cons
 // result keeps fp32 accuracy.  Gram matrices use the fp64 MFMA.
 typedef double double4_t __attribute__((ext_vector_type(4)));
 
-__device__ __forceinline__ void split16(float v, h16& hi, h16& lo) {
-  hi = (h16)v;
-  lo = (h16)(v - (float)hi);
-}
-
-// split16 of eight values, converted in pairs (packed fp32 -> fp16
-// conversions; the subtraction stays scalar fp32).
+// Eight fp32 values split into fp16 hi = (h16)v and lo = (h16)(v - hi),
+// converted in pairs (packed fp32 -> fp16 conversions; the subtraction stays
+// scalar fp32).
 typedef float f32x2_t __attribute__((ext_vector_type(2)));
 typedef _Float16 f16x2_t __attribute__((ext_vector_type(2)));
 __device__ __forceinline__ void split16x8(const float (&v)[8], half8_t& hi, half8_t& lo) {
