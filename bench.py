@@ -500,15 +500,52 @@ def model_loop(torch, device, prompt, decode_steps, layers=32):
         out, pre_s = timed(lambda: model(input_ids=ids[:, :n_prompt], use_cache=False, logits_to_keep=1))
         tok = out.logits[:, -1].argmax(-1)
         pos_all = torch.arange(n_prompt, n_prompt + steps, device=device)[None]   # positions stay on the device
+        toks = []
         torch.cuda.synchronize()
         t = time.perf_counter()
         for i in range(steps):
             out = model(input_ids=tok[:, None], position_ids=pos_all[:, i:i + 1], use_cache=False,
                         logits_to_keep=1)
             tok = out.logits[:, -1].argmax(-1)
+            toks.append(tok)
         host_s = time.perf_counter() - t          # the host issued every step without waiting
         torch.cuda.synchronize()
-        return pre_s, time.perf_counter() - t, host_s
+        return pre_s, time.perf_counter() - t, host_s, torch.cat(toks)
+
+    @torch.no_grad()
+    def graph_run(n_prompt, steps):
+        """The same greedy steps replayed from HIP graphs (CapturedDecode): one
+        captured segment per stretch between block boundaries; the step that
+        crosses a boundary (its append compresses) runs eagerly."""
+        from unsloth_spectral import CapturedDecode
+        for layer in model.model.layers:
+            layer.self_attn._spectral_cache = None
+        out = model(input_ids=ids[:, :n_prompt], use_cache=False, logits_to_keep=1)
+        tok = out.logits[:, -1].argmax(-1)
+        pos = torch.full((1, 1), n_prompt, dtype=torch.long, device=device)
+        toks, done, segments = [], 0, 0
+        torch.cuda.synchronize()
+        t = time.perf_counter()
+        while done < steps:
+            tail = model.model.layers[0].self_attn._spectral_cache.hot_len
+            seg = min(steps - done, TB - 1 - tail)
+            if seg >= 3:
+                dec = CapturedDecode(model, seg)
+                segments += 1
+                for _ in range(seg):
+                    tok = dec.step(tok, pos).argmax(-1)
+                    pos += 1
+                    toks.append(tok)
+            else:
+                seg = max(seg, 1)
+                for _ in range(seg):
+                    out = model(input_ids=tok[:, None], position_ids=pos, use_cache=False, logits_to_keep=1)
+                    tok = out.logits[:, -1].argmax(-1)
+                    pos += 1
+                    toks.append(tok)
+            done += seg
+        torch.cuda.synchronize()
+        return time.perf_counter() - t, torch.cat(toks), segments
 
     dense_run(min(prompt, 1024), 4)                      # warm-up (kernels, allocator)
     dense_s = dense_run(prompt, decode_steps)
@@ -516,9 +553,14 @@ def model_loop(torch, device, prompt, decode_steps, layers=32):
     torch.cuda.empty_cache()
     patch_unsloth_attention(model, k_rank_keys=16, k_rank_values=16, verbose=False, quant_granularity="per_row")
     spectral_run(min(prompt, 1024) + 8, 4)
-    prefill_s, spec_s, host_s = spectral_run(prompt, decode_steps)
+    prefill_s, spec_s, host_s, spec_tok = spectral_run(prompt, decode_steps)
     log(f"spectral cache: {spec_s / decode_steps * 1e3:.2f} ms per token, prefill {prefill_s:.2f} s")
     st = get_cache_stats(model)
+    graph_run(min(prompt, 1024) + 8, 8)                   # warm-up of the captured path
+    graph_s, graph_tok, graph_segments = graph_run(prompt, decode_steps)
+    same = (graph_tok == spec_tok).float().mean().item()
+    log(f"spectral cache, graph-replayed steps: {graph_s / decode_steps * 1e3:.2f} ms per token "
+        f"({graph_segments} captured segments), same tokens as the eager steps: {same:.3f}")
     # decode attention of one token over every layer's final cache (HIP events)
     from unsloth_spectral import _lib
     from unsloth_spectral._decode import run_decode
@@ -563,6 +605,13 @@ def model_loop(torch, device, prompt, decode_steps, layers=32):
                      "compression_ratio": round(st["compression_ratio"], 3),
                      "attention_ms_per_token": round(attn_ms, 3),
                      "attention_share": round(attn_ms / (spec_s / decode_steps * 1e3), 4)},
+        "spectral_graph_replay": {"decode_ms_per_token": round(graph_s / decode_steps * 1e3, 3),
+                                  "tokens_per_s": round(decode_steps / graph_s, 2),
+                                  "captured_segments": graph_segments,
+                                  "same_tokens_as_eager_fraction": round(same, 4),
+                                  "note": "unsloth_spectral.CapturedDecode: each stretch of steps between "
+                                          "block boundaries captured once (the capture is inside the timed "
+                                          "region) and replayed; greedy argmax between replays"},
         "dense_fp16_kv": {"decode_ms_per_token": round(dense_s / decode_steps * 1e3, 3),
                           "tokens_per_s": round(decode_steps / dense_s, 2)},
         "model_init_s": round(init_s, 1),

@@ -29,9 +29,10 @@ from .kernels import (  # noqa: E402
     spectral_score_forward,
     spectral_value_forward,
 )
-from .integration import get_cache_stats, patch_unsloth_attention  # noqa: E402
+from .integration import CapturedDecode, get_cache_stats, patch_unsloth_attention  # noqa: E402
 
 __all__ = [
+    "CapturedDecode",
     "SpectralCache",
     "SpectralBlock",
     "spectral_attention_forward",

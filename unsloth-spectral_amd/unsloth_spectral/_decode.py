@@ -93,7 +93,10 @@ def run_decode(Q, cache, cos, sin, query_position, attention_mask=None, scale=No
     a.q_heads = Hq
     a.rope_mode = rope_mode
     a.grid_blocks = cache._n_cold
-    a.grid_tail = cache._tail_len
+    # a pinned grid (captured decode segments) covers the tail tokens of every
+    # replayed step; workgroups past the device's tail length write neutral
+    # records
+    a.grid_tail = cache._tail_len if cache._grid_tail is None else max(cache._tail_len, cache._grid_tail)
     a.scale = float(scale)
     a.split = int(split)
     a.q = q.data_ptr()

@@ -332,3 +332,110 @@ def get_cache_stats(model):
     return {"total_tokens": total_tokens, "total_blocks": total_blocks, "total_original_bytes": orig,
             "total_compressed_bytes": comp, "compression_ratio": orig / comp if comp > 0 else 1.0,
             "layers_with_cache": len(per_layer), "per_layer_stats": per_layer}
+
+
+class CapturedDecode:
+    """One-token decode steps of a patched model replayed from a HIP graph.
+
+    The reference issues every decode step from Python (integration.py:596-659
+    per layer); at batch 1 that host work, not the GPU, sets the token rate.
+    Here one step of the whole model (every layer's append, spectral decode
+    attention, projections and MLP) is captured once with
+    ``torch.cuda.CUDAGraph`` and replayed for the following steps.  That is
+    valid because the append and decode kernels take positions, tail lengths
+    and block counts from the device counters; the only host-side launch
+    arguments that change from step to step are the decode grid's extents,
+    so each cache's tail grid is pinned for the segment (``steps`` tokens:
+    workgroups past the device's tail length write neutral records) and the
+    host mirror of the counters is advanced by the replays.
+
+    Usage, after the prompt has been run through the patched model::
+
+        dec = CapturedDecode(model, steps)
+        for i in range(steps):
+            logits = dec.step(token, position)   # [B, vocab]
+            token, position = logits.argmax(-1), position + 1
+
+    The first ``step`` runs eagerly (it also sizes the workspaces); the
+    second captures; later ones replay.  ``token`` ([B] or [B, 1]) and
+    ``position`` ([B, 1]) are device tensors; the returned logits of a replay
+    live in the graph's static output, valid until the next ``step``.  The
+    segment must not cross a block boundary (no compression inside it: every
+    cache's tail length plus ``steps`` stays below ``block_size``), and the
+    caches must hold room for it (``reserve``, as the prompt call does).
+    ``close()`` (or the last step) unpins the grids."""
+
+    def __init__(self, model, steps: int):
+        self.model = model
+        self.steps = int(steps)
+        self.left = self.steps
+        self.modules = [m for m in model.modules() if isinstance(getattr(m, "_spectral_cache", None), SpectralCache)]
+        if not self.modules:
+            raise ValueError("no spectral caches yet: run the prompt through the patched model first")
+        self.caches = [m._spectral_cache for m in self.modules]
+        for c in self.caches:
+            if c._B is None:
+                raise ValueError("empty spectral cache")
+            if c._tail_len + self.steps >= c.block_size:
+                raise ValueError(f"{self.steps} steps from a tail of {c._tail_len} cross a block boundary "
+                                 f"({c.block_size}): split the segment at the compression")
+            if c._tail_len + self.steps > c._tail_cap:
+                raise ValueError("the tail ring has no room for the segment: reserve() first")
+        for m, c in zip(self.modules, self.caches):
+            tab = getattr(m, "_spectral_rope", None)
+            if tab is not None:  # the tables must not be rebuilt inside the graph
+                tab.get(c.current_position + self.steps + 2, c.device)
+            c._grid_tail = c._tail_len + self.steps
+        self.graph = None
+        self.tok = self.pos = self.logits = None
+        # A prepared 4-D mask is passed through by transformers as is, so no
+        # mask is built inside the graph (building one copies a host scalar
+        # to the device, which a capture refuses); the patched attention does
+        # not read the mask of a one-token step (the cache keeps the prompt's
+        # key flags).
+        self.mask = None
+
+    def _forward(self, token, position):
+        if self.mask is None or self.mask.shape[0] != token.shape[0]:
+            dtype = next(self.model.parameters()).dtype
+            self.mask = torch.zeros(token.shape[0], 1, 1, 1, dtype=dtype, device=token.device)
+        out = self.model(input_ids=token, position_ids=position, attention_mask=self.mask, use_cache=False,
+                         logits_to_keep=1)
+        return out.logits[:, -1]
+
+    def _advance(self, n):
+        for c in self.caches:
+            c.total_tokens += n
+            c.current_position += n
+            c._tail_len += n
+
+    @torch.no_grad()
+    def step(self, token, position):
+        if self.left <= 0:
+            raise RuntimeError("the captured segment is used up")
+        token = token.reshape(-1, 1)
+        if self.left == self.steps:  # warm-up: eager, with the pinned grids
+            logits = self._forward(token, position)
+        else:
+            if self.graph is None:
+                self.tok = token.clone()
+                self.pos = position.clone()
+                g = torch.cuda.CUDAGraph()
+                with torch.cuda.graph(g):
+                    self.logits = self._forward(self.tok, self.pos)
+                self._advance(-1)  # the capture ran the host side of a step, not its kernels
+                self.graph = g
+            self.tok.copy_(token)
+            self.pos.copy_(position)
+            self.graph.replay()
+            self._advance(1)
+            logits = self.logits
+        self.left -= 1
+        if self.left == 0:
+            self.close()
+        return logits
+
+    def close(self):
+        for c in self.caches:
+            c._grid_tail = None
+        self.left = 0

@@ -162,6 +162,10 @@ class SpectralCache:
         self._tail_len = 0
         self._tail_head = 0
         self.key_mask = None
+        # Decode grid pinned for a captured (graph-replayed) decode segment:
+        # the decode launch covers this many tail tokens whatever the host
+        # mirror says (None = the mirror's tail length).
+        self._grid_tail = None
 
     def _allocate(self, batch):
         B, H, D, TB, NB, C = batch, self.num_heads, self.head_dim, self.block_size, self._max_blocks, self._tail_cap
