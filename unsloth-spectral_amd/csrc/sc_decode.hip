@@ -440,13 +440,18 @@ __device__ __forceinline__ Lanes lane_roles(int n, int nrep) {
 }
 
 // P values of the four lanes of this lane's quad, in quad-lane order: the
-// fp16 B operand (tokens 4 g + {0..3}) of a 16x16x16 P.V MFMA.
+// fp16 B operand (tokens 4 g + {0..3}) of a 16x16x16 P.V MFMA.  Every lane's
+// DPP source lies in its own quad, so the moves leave no lane unwritten and
+// their `old` operand is never read: mov_dpp leaves it undefined, which
+// saves the zero-initialising move per DPP that update_dpp(0, ...) costs
+// here (reductions keep update_dpp: the compiler folds those DPP moves into
+// the max/add itself).
 __device__ __forceinline__ half4_t quad_gather_h4(float v, uint32_t psel) {
   const uint32_t x = (uint32_t)__builtin_bit_cast(uint16_t, (h16)v);
-  const uint32_t y = (uint32_t)__builtin_amdgcn_update_dpp(0, (int)x, 0xB1, 0xF, 0xF, false);  // lane ^ 1
+  const uint32_t y = (uint32_t)__builtin_amdgcn_mov_dpp((int)x, 0xB1, 0xF, 0xF, false);  // lane ^ 1
   const uint32_t pair = __builtin_amdgcn_perm(x, y, psel);  // (even, odd) quad lane of this pair
-  const uint32_t lo = (uint32_t)__builtin_amdgcn_update_dpp(0, (int)pair, 0x00, 0xF, 0xF, false);  // quad lane 0
-  const uint32_t hi = (uint32_t)__builtin_amdgcn_update_dpp(0, (int)pair, 0xAA, 0xF, 0xF, false);  // quad lane 2
+  const uint32_t lo = (uint32_t)__builtin_amdgcn_mov_dpp((int)pair, 0x00, 0xF, 0xF, false);  // quad lane 0
+  const uint32_t hi = (uint32_t)__builtin_amdgcn_mov_dpp((int)pair, 0xAA, 0xF, 0xF, false);  // quad lane 2
   return __builtin_bit_cast(half4_t, make_uint2(lo, hi));
 }
 
