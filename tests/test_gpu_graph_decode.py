@@ -2,8 +2,8 @@
 
 A patched transformers MistralForCausalLM (random fp16 weights; 2 layers,
 8 query / 2 KV heads of dim 128) runs a 600-token prompt (one cold block
-plus an 88-token tail per layer), then 12 teacher-forced one-token steps
-three ways from the same cache state:
+plus an 88-token tail per layer) for one or two sequences, then 12
+teacher-forced one-token steps three ways from the same cache state:
   * CapturedDecode: one eager warm-up step, one capture, ten replays, with
     eager work (argmax, a copy) and a synchronisation between replays;
   * eager steps with the same pinned decode grid: every step's logits must be
@@ -39,13 +39,14 @@ def _restore(model, caches):
         layer.self_attn._spectral_cache = c.clone()
 
 
+@pytest.mark.parametrize("batch", [1, 2])
 @torch.no_grad()
-def test_captured_decode_replays_match_eager_steps():
+def test_captured_decode_replays_match_eager_steps(batch):
     from unsloth_spectral import CapturedDecode, _lib, patch_unsloth_attention
     model = _model()
     n_prompt, steps = 600, 12
     g = torch.Generator().manual_seed(6)
-    ids = torch.randint(0, VOCAB, (1, n_prompt + steps), generator=g).cuda()
+    ids = torch.randint(0, VOCAB, (batch, n_prompt + steps), generator=g).cuda()
     patch_unsloth_attention(model, use_triton_kernel=True, verbose=False)
     model(input_ids=ids[:, :n_prompt], use_cache=False, logits_to_keep=1)
     snap = _snapshot(model)
@@ -56,7 +57,7 @@ def test_captured_decode_replays_match_eager_steps():
         return ids[:, n_prompt + i]
 
     def position(i):
-        return torch.full((1, 1), n_prompt + i, dtype=torch.long, device="cuda")
+        return torch.full((batch, 1), n_prompt + i, dtype=torch.long, device="cuda")
 
     # graph-replayed segment
     dec = CapturedDecode(model, steps)
@@ -71,7 +72,7 @@ def test_captured_decode_replays_match_eager_steps():
     for c in after:
         assert c._grid_tail is None
         assert c.hot_len == n_prompt - 512 + steps and c.current_position == n_prompt + steps
-        assert c.counters[:, _lib.SC_CNT_TAIL_LEN].tolist() == [c.hot_len]  # device tail length = host mirror
+        assert c.counters[:, _lib.SC_CNT_TAIL_LEN].tolist() == [c.hot_len] * batch  # device = host mirror
     graph_logits = torch.stack(graph_logits)
 
     # eager steps, same pinned grid, from the same cache state
