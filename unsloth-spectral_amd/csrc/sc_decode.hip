@@ -1142,9 +1142,11 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(2))) v
 // Log-sum-exp merge of the partial records of one (sequence, query head):
 // one single-wave workgroup per query head, lane l owns d = E l .. E l + E - 1.
 // Records are merged U at a time with every load of a chunk in flight at
-// once: lane k (and k + U) loads the (m, l) header of record k, the chunk
-// maximum and the weighted sum of l are register reductions, and the weight of
-// record k reaches every lane by readlane (an SGPR operand of the FMAs).
+// once: lane k (and k + 32 when U = 32) loads the (m, l) header of record k,
+// the chunk maximum and the weighted sum of l are register reductions, and
+// the weight of record k reaches every lane by readlane (an SGPR operand of
+// the FMAs).  U = 64 when there are more than 32 records: each dependent
+// round of loads then covers twice the records.
 // Every unit writes its record (m = -inf, l = 0, o = 0 when it saw no
 // token), so a weight of zero needs no branch.
 // Reduction over each 32-lane half of a wavefront in registers: DPP quad
@@ -1162,11 +1164,24 @@ __device__ __forceinline__ float half_reduce(float v) {
   return op(__uint_as_float(b[0]), __uint_as_float(b[1]));
 }
 
-template <int D>
+// Reduction of the chunk's headers: each 32-lane half (U = 32: both halves
+// hold the same headers), or the whole wave (U = 64).
+template <bool MAX, int U>
+__device__ __forceinline__ float chunk_reduce(float v) {
+  static_assert(U == 32 || U == 64, "one header per lane of a half or of the wave");
+  v = half_reduce<MAX>(v);
+  if constexpr (U == 64) {
+    const uint32_t u = __float_as_uint(v);
+    auto a = __builtin_amdgcn_permlane32_swap(u, u, false, false);
+    v = MAX ? fmaxf(__uint_as_float(a[0]), __uint_as_float(a[1])) : __uint_as_float(a[0]) + __uint_as_float(a[1]);
+  }
+  return v;
+}
+
+template <int D, int U>
 __global__ __launch_bounds__(64) void decode_combine_kernel(DecodeParams p) {
   constexpr int PREC = Geo<D>::PREC;
   constexpr int E = D / 64;  // d values per lane
-  constexpr int U = 32;      // records per chunk (lanes k and k + 32 hold header k)
   const int wq = blockIdx.x;
   const int b = wq / p.Hq, qh = wq % p.Hq;
   const int h = qh / p.nrep, hh = qh % p.nrep;
@@ -1199,12 +1214,11 @@ __global__ __launch_bounds__(64) void decode_combine_kernel(DecodeParams p) {
     // scheduler sinks them to their uses and the chunk costs two round trips.
     __builtin_amdgcn_sched_barrier(0);
     const float mk = has ? ml.x : -INFINITY;
-    static_assert(U == 32, "one header per lane of each 32-lane half");
-    const float mc = half_reduce<true>(mk);
+    const float mc = chunk_reduce<true, U>(mk);
     const float mn = fmaxf(M, mc);
     if (mn == -INFINITY) continue;  // wave-uniform: nothing seen yet
     const float ck = mk == -INFINITY ? 0.f : fast_exp2(mk - mn);
-    const float lc = half_reduce<false>(has ? ml.y * ck : 0.f);
+    const float lc = chunk_reduce<false, U>(has ? ml.y * ck : 0.f);
     const float a = fast_exp2(M - mn);  // exp2(-inf) = 0 on the first chunk
     L = L * a + lc;
 #pragma unroll
@@ -1375,7 +1389,10 @@ int launch(DecodeParams& p, hipStream_t s) {
     int rc = sc_launch_status("decode_partial_kernel");
     if (rc) return rc;
   }
-  hipLaunchKernelGGL((decode_combine_kernel<D>), dim3(p.B * p.Hq), dim3(64), 0, s, p);
+  if (p.units_per_bh > 32)
+    hipLaunchKernelGGL((decode_combine_kernel<D, 64>), dim3(p.B * p.Hq), dim3(64), 0, s, p);
+  else
+    hipLaunchKernelGGL((decode_combine_kernel<D, 32>), dim3(p.B * p.Hq), dim3(64), 0, s, p);
   return sc_launch_status("decode_combine_kernel");
 }
 
