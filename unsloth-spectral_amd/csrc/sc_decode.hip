@@ -1053,19 +1053,29 @@ __device__ void cold_unit(const DecodeParams& p, int b, int hq, int j, char* sme
       for (int nt = 0; nt < NT; ++nt)
         bvf[mt][nt] = *reinterpret_cast<const half4_t*>(bvb + (long)(16 * mt + n) * KV + 16 * nt + 4 * g);
   };
+  // With the smaller ranks of the branch-free path the tail tile's RoPE
+  // entries (its positions arrived during the range before) are requested
+  // before the last range, whose step stages no rows and refills no codes,
+  // so they arrive while it computes; elsewhere the registers are not there
+  // (k = 32/32: 36 spills) and they follow the last range.
+  constexpr bool kEarlyTailRope = !GEN && KK + KV <= 48;
   if (nR > 2) {
     step(TT(), TT(), nR - 2);
     load_bv();
+    if constexpr (kEarlyTailRope) tail_fetch_rope<D, HE>(p, rope, tf);
     step(FF(), TT(), nR - 1);
   } else if (nR == 2) {
     step(TT(), FF(), 0);
     load_bv();
+    if constexpr (kEarlyTailRope) tail_fetch_rope<D, HE>(p, rope, tf);
     step(FF(), TT(), 1);
   } else {
     load_bv();
+    if constexpr (kEarlyTailRope) tail_fetch_rope<D, HE>(p, rope, tf);
     step(FF(), FF(), 0);
   }
-  tail_fetch_rope<D, HE>(p, rope, tf);  // positions arrived during the last ranges (unconditional: no branch)
+  if constexpr (!kEarlyTailRope)
+    tail_fetch_rope<D, HE>(p, rope, tf);  // positions arrived during the last ranges (unconditional: no branch)
   if (hvalid) range_values<KV, TPW, GEN, PRM, false>(p, cb0, CodeSrc{}, lgp, msp, alp, vn, st);
   if (!hvalid) return;
   // ---- FP16 tail tiles of this workgroup, merged into the running state
