@@ -213,6 +213,25 @@ int sc_block_values(const float* attn, int64_t attn_stride_b, int64_t attn_strid
                     int32_t rank, int32_t head_dim, void* out, void* stream);
 
 /*
+ * Query rotation of a decode or prefill step: what the reference's
+ * apply_rotary_pos_emb (integration.py:428-465) computes for the queries
+ * where its decode caller rotates them (integration.py:610-613), in one
+ * launch instead of five elementwise tensor ops:
+ *   out = x * cos + rotate_half(x) * sin,  rotate_half(x) = (-x2, x1),
+ * each product and the sum rounded to fp16 in that order (bit-identical to
+ * the fp16 tensor expression).
+ *   x        fp16 [batch][heads][tokens][head_dim], element strides
+ *   cos/sin  fp16 [batch][tokens][head_dim], element strides (cs_stride_b = 0
+ *            shares one set of rows across the batch)
+ *   out      fp16 [batch][heads][tokens][head_dim], contiguous
+ * Rows 16-byte aligned (strides multiples of 8).  Supported: head_dim a
+ * multiple of 16 in [16, 256].
+ */
+int sc_rope_rotate(const void* x, int64_t x_stride_b, int64_t x_stride_h, int64_t x_stride_t, const void* cos,
+                   const void* sin, int64_t cs_stride_b, int64_t cs_stride_t, int32_t batch, int32_t heads,
+                   int32_t tokens, int32_t head_dim, void* out, void* stream);
+
+/*
  * Batched block compression: randomized SVD (rsvd.py:74-157, k = rank,
  * oversampling, n_iter) of `count` matrices [rows][cols] (fp16, fp32 or
  * bf16 per m_dtype; computed in fp32 like rsvd.py:79-81), then

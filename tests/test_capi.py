@@ -25,7 +25,7 @@ def test_header_declares_the_api():
     for fn in ("sc_decode_attn", "sc_decode_workspace_size", "sc_rsvd_compress", "sc_quantize_int8",
                "sc_tier_append", "sc_tier_compress", "sc_tier_dequant", "sc_last_error", "sc_abi_version",
                "sc_block_record_bytes", "sc_tier_pack", "sc_tier_unpack", "sc_prefill_attn", "sc_block_scores",
-               "sc_block_values"):
+               "sc_block_values", "sc_rope_rotate"):
         assert fn in names
 
 
@@ -79,3 +79,6 @@ def test_host_side_checks_refuse_bad_calls_without_a_gpu():
     assert lib.sc_block_values(None, 0, 0, 1, 8, None, None, 3, 16, 8, 128, None, None) == -1    # 8 % 3
     assert b"multiple" in lib.sc_last_error()
     assert lib.sc_block_values(None, 0, 0, 1, 8, None, None, 2, 16, 65, 128, None, None) == -2   # rank > 64
+    assert lib.sc_rope_rotate(None, 0, 0, 0, None, None, 0, 0, 1, 8, 1, 120, None, None) == -2  # head_dim % 16
+    assert lib.sc_rope_rotate(None, 0, 0, 0, None, None, 0, 0, 1, 8, 1, 128, None, None) == -1  # null pointers
+    assert lib.sc_rope_rotate(None, 0, 0, 0, None, None, 0, 0, 1, 0, 1, 128, None, None) == 0   # nothing to do

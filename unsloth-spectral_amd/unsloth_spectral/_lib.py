@@ -104,6 +104,8 @@ PROTOTYPES = {
                                 c_i64, c_i32, c_i32, c_vp, c_vp]),
     "sc_block_values": (c_i32, [c_vp, c_i64, c_i64, c_i32, c_i32, c_vp, c_vp, c_i32, c_i32, c_i32, c_i32, c_vp,
                                 c_vp]),
+    "sc_rope_rotate": (c_i32, [c_vp, c_i64, c_i64, c_i64, c_vp, c_vp, c_i64, c_i64, c_i32, c_i32, c_i32, c_i32, c_vp,
+                               c_vp]),
     "sc_last_error": (ctypes.c_char_p, []),
     "sc_abi_version": (c_i32, []),
 }
