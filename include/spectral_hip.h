@@ -112,7 +112,8 @@ typedef struct ScTierDesc {
  * (spectral_attention.py:117-349, rope_mode = SC_ROPE_DISTANCE).
  *   q          fp16 [batch][q_heads][head_dim] (post-RoPE), element strides
  *   cos/sin    fp16 [rope_len][head_dim] RoPE tables (row stride rope_stride)
- *   query_pos  int32 [batch] device array, or NULL to use query_pos_scalar
+ *   query_pos  int32 [batch] device array (int64 with query_pos_i64 != 0), or
+ *              NULL to use query_pos_scalar
  *   mask       optional uint8 keep-mask (0 = drop, reference
  *              spectral_attention.py:284-285) indexed [b][h][token] in
  *              cache order (cold blocks, then tail); NULL = no mask
@@ -156,6 +157,8 @@ typedef struct ScDecodeArgs {
   float* logits_out;
   int64_t logits_stride_b, logits_stride_h;
   int32_t split;
+  int32_t query_pos_i64;  /* nonzero: query_pos points to int64_t[batch] (a model's
+                             position ids as they are); 0: int32_t[batch] */
 } ScDecodeArgs;
 
 int sc_decode_workspace_size(const ScDecodeArgs* args, size_t* bytes);

@@ -46,6 +46,9 @@ def test_struct_layouts_match_header():
     assert ctypes.sizeof(_lib.ScTierDesc) == 11 * 4 + 4 + 14 * 8
     assert _lib.ScTierDesc.codes_k.offset == 48
     assert _lib.ScDecodeArgs.scale.offset == 24 and _lib.ScDecodeArgs.q.offset == 32
+    # query_pos_i64 sits in the tail padding after split: the size is unchanged
+    assert _lib.ScDecodeArgs.query_pos_i64.offset == _lib.ScDecodeArgs.split.offset + 4
+    assert ctypes.sizeof(_lib.ScDecodeArgs) == _lib.ScDecodeArgs.split.offset + 8 == 184
     assert _lib.ScCompressArgs.m.offset == 48
 
 

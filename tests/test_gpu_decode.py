@@ -136,6 +136,32 @@ def test_per_sequence_query_positions_on_device():
     _check(states, Q, cos, sin, q, "distance", block_size=128, qpos_tensor=True)
 
 
+def test_int64_query_positions_equal_int32():
+    """A model's int64 position ids reach the kernel as they are
+    (query_pos_i64, no conversion launch): the same output bits as int32
+    positions, which the oracle check above covers; a strided int64 view is
+    converted instead and gives the same bits too."""
+    from unsloth_spectral import _lib
+    from unsloth_spectral._decode import run_decode
+    rng = np.random.default_rng(18)
+    states = [random_state(rng, 2, 128, 2, 128, 16, 32, 50, start=s) for s in (0, 1000)]
+    cos, sin = rope_tables(2000, 128)
+    Q16 = rng.standard_normal((2, 8, 128)).astype(np.float16)
+    q = [states[0].total_tokens() - 1, 1000 + states[1].total_tokens() - 1]
+    _check(states, Q16, cos, sin, q, "distance", block_size=128, qpos_tensor=True)
+    cache = cache_from_states(states, 128)
+    ct, st = tables(cos, sin)
+    Q = torch.from_numpy(Q16).cuda().reshape(2, 8, 1, 128)
+    code = _lib.SC_ROPE_DISTANCE
+    ref = run_decode(Q, cache, ct, st, torch.tensor(q, dtype=torch.int32, device="cuda"), None, None, code)
+    ids = torch.tensor([[p] for p in q], dtype=torch.int64, device="cuda")        # [B, 1] like a model's
+    got = run_decode(Q, cache, ct, st, ids[:, -1], None, None, code)
+    wide = torch.tensor([[0, p] for p in q], dtype=torch.int64, device="cuda")    # [:, -1] has stride 2
+    got2 = run_decode(Q, cache, ct, st, wide[:, -1], None, None, code)
+    torch.cuda.synchronize()
+    assert torch.equal(got, ref) and torch.equal(got2, ref)
+
+
 def test_unequal_table_halves_use_full_rows():
     rng = np.random.default_rng(9)
     states = [random_state(rng, 2, 128, 2, 128, 16, 32, 40)]

@@ -82,7 +82,7 @@ struct DecodeParams {
   const h16* sin;
   long rope_stride;
   const int32_t* qpos;
-  int qpos_scalar;
+  int qpos_scalar, qpos64;  // qpos64: qpos points to int64 positions
   const uint8_t* mask;
   long mask_sb, mask_sh;
   float* logits;
@@ -950,7 +950,7 @@ __device__ void cold_unit(const DecodeParams& p, int b, int hq, int j, char* sme
   }
   const long bhj = (long)(b * p.Hkv + (hvalid ? h : 0)) * p.NB + jb;
   const int start = p.block_start[b * p.NB + jb];
-  const int qp = p.qpos ? p.qpos[b] : p.qpos_scalar;
+  const int qp = !p.qpos ? p.qpos_scalar : p.qpos64 ? (int)reinterpret_cast<const int64_t*>(p.qpos)[b] : p.qpos[b];
   const bool dist = p.rope_mode == SC_ROPE_DISTANCE;
   const bool rope = !GEN || p.rope_mode != SC_ROPE_NONE;
   constexpr int RBUF = T * RS::ROW;  // bytes of one staged range
@@ -1346,6 +1346,7 @@ int fill_params(const ScDecodeArgs* a, DecodeParams* p) {
   p->rope_stride = a->rope_stride;
   p->qpos = a->query_pos;
   p->qpos_scalar = a->query_pos_scalar;
+  p->qpos64 = a->query_pos_i64 != 0;
   p->mask = a->mask;
   p->mask_sb = a->mask_stride_b;
   p->mask_sh = a->mask_stride_h;

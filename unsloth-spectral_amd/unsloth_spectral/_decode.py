@@ -113,8 +113,12 @@ def run_decode(Q, cache, cos, sin, query_position, attention_mask=None, scale=No
         a.halves_equal = int(_halves_equal(cos16, sin16) if halves_equal is None else halves_equal)
         keep += [cos16, sin16]
     if isinstance(query_position, torch.Tensor):
-        qp = query_position.to(device=Q.device, dtype=torch.int32).reshape(-1)
-        qp = qp.expand(B).contiguous() if qp.numel() == 1 else qp.contiguous()
+        qp = query_position.reshape(-1)
+        if qp.dtype == torch.int64 and qp.device == Q.device and qp.numel() == B and (B == 1 or qp.stride(0) == 1):
+            a.query_pos_i64 = 1          # a model's position ids as they are (no conversion launch)
+        else:
+            qp = qp.to(device=Q.device, dtype=torch.int32)
+            qp = qp.expand(B).contiguous() if qp.numel() == 1 else qp.contiguous()
         a.query_pos = qp.data_ptr()
         keep.append(qp)
     else:

@@ -53,7 +53,7 @@ class ScDecodeArgs(ctypes.Structure):
         ("mask", c_vp), ("mask_stride_b", c_i64), ("mask_stride_h", c_i64),
         ("out", c_vp), ("out_stride_b", c_i64), ("out_stride_h", c_i64),
         ("logits_out", c_vp), ("logits_stride_b", c_i64), ("logits_stride_h", c_i64),
-        ("split", c_i32),
+        ("split", c_i32), ("query_pos_i64", c_i32),
     ]
 
 
@@ -153,7 +153,14 @@ def require_device(t, name):
 
 
 def stream_of(t):
-    return ctypes.c_void_p(torch.cuda.current_stream(t.device).cuda_stream)
+    """The current HIP stream of t's device, as a handle for the C ABI."""
+    return ctypes.c_void_p(_raw_stream(t.device.index if t.device.index is not None else torch.cuda.current_device()))
+
+
+# torch's raw current-stream query skips building a Stream object (a few
+# microseconds per launch on the host); the public call is the fallback.
+_raw_stream = getattr(torch._C, "_cuda_getCurrentRawStream", None) or \
+    (lambda index: torch.cuda.current_stream(index).cuda_stream)
 
 
 def ptr(t):
