@@ -318,7 +318,9 @@ int sc_quantize_int8(const float* x, int64_t groups, int64_t rows, int64_t cols,
  *                          (the caller detected the restart, as the
  *                          reference does on the host, :176-189);
  *   SC_APPEND_DETECT_RESET the device detects it per sequence: a first
- *                          position below NEXT_POS resets that sequence.
+ *                          position below NEXT_POS resets that sequence;
+ *   SC_APPEND_POS_I64      positions points to int64 [batch][t_new] (a
+ *                          model's position ids as they are).
  * Fails with SC_ERR_CAPACITY (before launching) if t_new exceeds the ring.
  * On the device, a sequence whose tail would exceed tail_capacity gets
  * nothing written, keeps its counters and has SC_CNT_STATUS set to
@@ -327,6 +329,7 @@ int sc_quantize_int8(const float* x, int64_t groups, int64_t rows, int64_t cols,
  */
 #define SC_APPEND_DETECT_RESET 1
 #define SC_APPEND_RESET 2
+#define SC_APPEND_POS_I64 4
 int sc_tier_append(const ScTierDesc* tier, const void* k_new, const void* v_new,
                    int64_t stride_b, int64_t stride_h, int64_t stride_t,
                    const int32_t* positions, int32_t t_new, int32_t flags, void* stream);

@@ -51,6 +51,28 @@ def test_append_counts_positions_and_tail_match_oracle():
     assert [b.start_position for b in cache.cold_blocks] == [b.start for b in tm.blocks]
 
 
+def test_int64_and_int32_positions_append_the_same_tiers():
+    """int64 position ids go to the append kernel as they are
+    (SC_APPEND_POS_I64); int32 ones, and int64 views that are not
+    contiguous, through the int32 array: the same tail rows, positions and
+    counters, including a device-detected new generation."""
+    rng = np.random.default_rng(5)
+    H, D, T = 2, 128, 128
+    caches = [_make(H, D, T, tail_capacity=512) for _ in range(3)]
+    for n, start in ((40, 0), (1, 40), (1, 41), (30, 7), (1, 37)):
+        K = torch.from_numpy(rng.standard_normal((2, H, n, D)).astype(np.float16)).cuda()
+        V = torch.from_numpy(rng.standard_normal((2, H, n, D)).astype(np.float16)).cuda()
+        p64 = torch.arange(start, start + n, device="cuda")[None].expand(2, n).contiguous()
+        wide = torch.stack([p64, p64], dim=-1)[..., 0]                       # int64, not contiguous
+        for c, p in zip(caches, (p64, p64.to(torch.int32), wide)):
+            c.append(K, V, p)
+    for c in caches[1:]:
+        assert torch.equal(c.counters, caches[0].counters)
+        assert torch.equal(c.tail_k, caches[0].tail_k) and torch.equal(c.tail_pos, caches[0].tail_pos)
+        assert c.total_tokens == caches[0].total_tokens and c.hot_len == caches[0].hot_len
+    assert caches[0].hot_position_ids[0].tolist() == list(range(7, 38))
+
+
 def test_low_rank_blocks_reconstruct():
     rng = np.random.default_rng(1)
     H, D, T, r = 2, 128, 128, 6

@@ -16,10 +16,16 @@ struct AppendParams {
   const h16* k_new;
   const h16* v_new;
   long sb, sh, st;
-  const int32_t* positions;
+  const void* positions;  // int32, or int64 with SC_APPEND_POS_I64
   int t_new;
   int flags;
 };
+
+// Position i of the append's [batch][t_new] positions.
+__device__ __forceinline__ int append_pos(const AppendParams& p, long i) {
+  return (p.flags & SC_APPEND_POS_I64) ? (int)static_cast<const int64_t*>(p.positions)[i]
+                                       : static_cast<const int32_t*>(p.positions)[i];
+}
 
 // New generation: the caller says so (SC_APPEND_RESET), or, with
 // SC_APPEND_DETECT_RESET, the sequence's first new position lies below the
@@ -27,7 +33,7 @@ struct AppendParams {
 __device__ __forceinline__ bool append_resets(const AppendParams& p, const int32_t* cnt, int b) {
   if (p.flags & SC_APPEND_RESET) return true;
   return (p.flags & SC_APPEND_DETECT_RESET) && p.positions && cnt[SC_CNT_TOTAL] > 0 &&
-         p.positions[(long)b * p.t_new] < cnt[SC_CNT_NEXT_POS];
+         append_pos(p, (long)b * p.t_new) < cnt[SC_CNT_NEXT_POS];
 }
 
 // The rows fit the ring: tail length after the append <= capacity.
@@ -60,7 +66,7 @@ __global__ __launch_bounds__(kThreads) void append_copy_kernel(AppendParams p) {
              (((long)b * p.t.kv_heads + h) * p.t.tail_capacity + slot) * D + chunk * 8;
   *reinterpret_cast<half8_t*>(dst) = *reinterpret_cast<const half8_t*>(src);
   if (h == 0 && chunk == 0 && kind == 0) {
-    const int pos = p.positions ? p.positions[(long)b * p.t_new + tt] : (reset ? 0 : cnt[SC_CNT_NEXT_POS]) + tt;
+    const int pos = p.positions ? append_pos(p, (long)b * p.t_new + tt) : (reset ? 0 : cnt[SC_CNT_NEXT_POS]) + tt;
     p.t.tail_pos[(long)b * p.t.tail_capacity + slot] = pos;
   }
 }
@@ -126,7 +132,8 @@ extern "C" int sc_tier_append(const ScTierDesc* t, const void* k_new, const void
   if (!t || !t->counters || !t->tail_k || !t->tail_v || !t->tail_pos)
     return sc_fail(SC_ERR_INVALID, "sc_tier_append: null tier");
   if (t_new < 0) return sc_fail(SC_ERR_INVALID, "negative t_new");
-  if (flags & ~(SC_APPEND_DETECT_RESET | SC_APPEND_RESET)) return sc_fail(SC_ERR_INVALID, "bad append flags %d", flags);
+  if (flags & ~(SC_APPEND_DETECT_RESET | SC_APPEND_RESET | SC_APPEND_POS_I64))
+    return sc_fail(SC_ERR_INVALID, "bad append flags %d", flags);
   if (t_new == 0) return SC_OK;
   if (t_new > t->tail_capacity)
     return sc_fail(SC_ERR_CAPACITY, "append of %d tokens exceeds the tail ring (%d)", t_new, t->tail_capacity);

@@ -19,7 +19,7 @@ SC_QUANT_PER_HEAD, SC_QUANT_PER_ROW, SC_QUANT_PER_TENSOR = 0, 1, 2
 SC_CNT_NCOLD, SC_CNT_TAIL_HEAD, SC_CNT_TAIL_LEN, SC_CNT_NEXT_POS = 0, 1, 2, 3
 SC_CNT_TOTAL, SC_CNT_COMPRESSIONS, SC_CNT_STATUS = 4, 5, 6
 SC_NCOUNTERS = 8
-SC_APPEND_DETECT_RESET, SC_APPEND_RESET = 1, 2
+SC_APPEND_DETECT_RESET, SC_APPEND_RESET, SC_APPEND_POS_I64 = 1, 2, 4
 SC_ERR_CAPACITY = -5
 SC_DECODE_SCRATCH_BYTES = 32 << 20
 

@@ -316,8 +316,13 @@ class SpectralCache:
         if position_ids is not None:
             if not isinstance(position_ids, torch.Tensor):
                 position_ids = torch.as_tensor(position_ids)
-            pos = position_ids.to(device=self.device, dtype=torch.int32).reshape(-1, T)
-            pos = pos.expand(B, T).contiguous() if pos.shape[0] != B else pos.contiguous()
+            pos = position_ids.reshape(-1, T)
+            if pos.dtype == torch.int64 and pos.device == self.device and pos.shape[0] == B and \
+                    pos.is_contiguous():
+                flags |= _lib.SC_APPEND_POS_I64     # a model's position ids as they are (no conversion launch)
+            else:
+                pos = pos.to(device=self.device, dtype=torch.int32)
+                pos = pos.expand(B, T).contiguous() if pos.shape[0] != B else pos.contiguous()
         self._grow_tail(self._tail_len + T)
         st = _lib.stream_of(K16)
         check(_lib.load().sc_tier_append(ctypes.byref(self._tier()), ptr(K16), ptr(V16), K16.stride(0),
