@@ -150,6 +150,22 @@ def test_append_overflow_sets_status_and_writes_nothing():
     cnt = cache.counters.cpu().numpy()
     assert (cnt[:, _lib.SC_CNT_STATUS] == 0).all() and (cnt[:, _lib.SC_CNT_TAIL_LEN] == 40).all()
     assert torch.equal(cache.tail_k[:, :, :40], K2)
+    # short appends (a decode step's tokens) take the one-launch path: the
+    # same refusal, status and untouched rows
+    K4 = torch.randn(2, 2, 87, 64, generator=g, device="cuda").half()
+    assert _append_raw(cache, K4, K4, None, 0) == 0          # 127 of 128
+    K5 = torch.randn(2, 2, 2, 64, generator=g, device="cuda").half()
+    torch.cuda.synchronize()
+    before_k = cache.tail_k.clone()
+    assert _append_raw(cache, K5, K5, None, 0) == 0          # 129 > 128: refused on the device
+    torch.cuda.synchronize()
+    cnt = cache.counters.cpu().numpy()
+    assert (cnt[:, _lib.SC_CNT_STATUS] == _lib.SC_ERR_CAPACITY).all() and (cnt[:, _lib.SC_CNT_TAIL_LEN] == 127).all()
+    assert torch.equal(cache.tail_k, before_k)
+    assert _append_raw(cache, K5[:, :, :1], K5[:, :, :1], None, 0) == 0   # 128: fits
+    torch.cuda.synchronize()
+    assert (cache.counters[:, _lib.SC_CNT_TAIL_LEN] == 128).all()
+    assert torch.equal(cache.tail_k[:, :, 127], K5[:, :, 0])
     # a single call larger than the ring is refused on the host
     K3 = torch.zeros(2, 2, 129, 64, dtype=torch.float16, device="cuda")
     assert _append_raw(cache, K3, K3, None, 0) == _lib.SC_ERR_CAPACITY

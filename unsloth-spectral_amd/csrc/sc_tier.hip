@@ -41,14 +41,9 @@ __device__ __forceinline__ bool append_fits(const AppendParams& p, const int32_t
   return (reset ? 0 : cnt[SC_CNT_TAIL_LEN]) + p.t_new <= p.t.tail_capacity;
 }
 
-// Work item = one 16-byte chunk of one K or V row.
-__global__ __launch_bounds__(kThreads) void append_copy_kernel(AppendParams p) {
+// Work item `rem` of sequence b = one 16-byte chunk of one K or V row.
+__device__ __forceinline__ void append_item(const AppendParams& p, int b, long rem) {
   const int D = p.t.head_dim, cpr = D / 8;
-  const long per_b = (long)p.t.kv_heads * p.t_new * cpr * 2;
-  const long idx = (long)blockIdx.x * kThreads + threadIdx.x;
-  if (idx >= per_b * p.t.batch) return;
-  const int b = (int)(idx / per_b);
-  long rem = idx % per_b;
   const int kind = (int)(rem % 2);
   rem /= 2;
   const int chunk = (int)(rem % cpr);
@@ -57,7 +52,7 @@ __global__ __launch_bounds__(kThreads) void append_copy_kernel(AppendParams p) {
   const int h = (int)(rem / p.t_new);
   const int32_t* cnt = p.t.counters + b * SC_NCOUNTERS;
   const bool reset = append_resets(p, cnt, b);
-  if (!append_fits(p, cnt, reset)) return;  // nothing written; the finalize kernel records the status
+  if (!append_fits(p, cnt, reset)) return;  // nothing written; the counter update records the status
   const int base_len = reset ? 0 : cnt[SC_CNT_TAIL_LEN];
   const int base_head = reset ? 0 : cnt[SC_CNT_TAIL_HEAD];
   const int slot = (base_head + base_len + tt) % p.t.tail_capacity;
@@ -71,9 +66,15 @@ __global__ __launch_bounds__(kThreads) void append_copy_kernel(AppendParams p) {
   }
 }
 
-__global__ void append_finalize_kernel(AppendParams p) {
-  const int b = blockIdx.x * blockDim.x + threadIdx.x;
-  if (b >= p.t.batch) return;
+__global__ __launch_bounds__(kThreads) void append_copy_kernel(AppendParams p) {
+  const long per_b = (long)p.t.kv_heads * p.t_new * (p.t.head_dim / 8) * 2;
+  const long idx = (long)blockIdx.x * kThreads + threadIdx.x;
+  if (idx >= per_b * p.t.batch) return;
+  append_item(p, (int)(idx / per_b), idx % per_b);
+}
+
+// Counter update of sequence b after its rows are written.
+__device__ __forceinline__ void append_counters(const AppendParams& p, int b) {
   int32_t* cnt = p.t.counters + b * SC_NCOUNTERS;
   const bool reset = append_resets(p, cnt, b);
   if (!append_fits(p, cnt, reset)) {  // ring overflow: counters unchanged, status set
@@ -86,6 +87,25 @@ __global__ void append_finalize_kernel(AppendParams p) {
   cnt[SC_CNT_TAIL_LEN] += p.t_new;
   cnt[SC_CNT_NEXT_POS] += p.t_new;
   cnt[SC_CNT_TOTAL] += p.t_new;
+}
+
+__global__ void append_finalize_kernel(AppendParams p) {
+  const int b = blockIdx.x * blockDim.x + threadIdx.x;
+  if (b >= p.t.batch) return;
+  append_counters(p, b);
+}
+
+// Short appends (a decode step's token): one workgroup per sequence writes
+// the sequence's rows, then, after a barrier, its counters.  Every thread
+// reads the counters before the barrier and only thread 0 writes them after
+// it, so the rows and the counter update need no second launch.
+__global__ __launch_bounds__(kThreads) void append_short_kernel(AppendParams p) {
+  const int b = blockIdx.x;
+  const int D = p.t.head_dim, cpr = D / 8;
+  const int per_b = p.t.kv_heads * p.t_new * cpr * 2;
+  for (int i = threadIdx.x; i < per_b; i += kThreads) append_item(p, b, i);
+  __syncthreads();
+  if (threadIdx.x == 0) append_counters(p, b);
 }
 
 struct DequantParams {
@@ -151,8 +171,13 @@ extern "C" int sc_tier_append(const ScTierDesc* t, const void* k_new, const void
   p.positions = positions;
   p.t_new = t_new;
   p.flags = flags;
-  const long items = (long)t->batch * t->kv_heads * t_new * (t->head_dim / 8) * 2;
+  const long per_b = (long)t->kv_heads * t_new * (t->head_dim / 8) * 2;
+  const long items = (long)t->batch * per_b;
   hipStream_t s = (hipStream_t)stream;
+  if (per_b <= 4 * kThreads) {  // one workgroup per sequence, counters in the same launch
+    hipLaunchKernelGGL(append_short_kernel, dim3((unsigned)t->batch), dim3(kThreads), 0, s, p);
+    return sc_launch_status("append_short_kernel");
+  }
   hipLaunchKernelGGL(append_copy_kernel, dim3((unsigned)((items + kThreads - 1) / kThreads)), dim3(kThreads), 0, s, p);
   int rc = sc_launch_status("append_copy_kernel");
   if (rc) return rc;
