@@ -1110,12 +1110,12 @@ __device__ __forceinline__ void jacobi_rotation(double app, double aqq, double a
 //     (at RM = 40 one round later, off the rotation chain); the players of a
 //     position move by one per round, so the two LDS offsets of an item are
 //     updated by one compare and select each.
-// Stops at a sweep boundary when the off-diagonal mass is <= 1e-10 of the
-// diagonal mass (the off-diagonal norm below 1e-5 of the diagonal's): the
-// eigenvectors then mix the retained and the dropped directions by ~1e-5,
-// which moves the reconstruction error of the truncated fit by ~1e-8
-// relative (second order), far below the fp32 and INT8 rounding of the
-// outputs.
+// Stops at a sweep boundary when the off-diagonal mass is <= 1e-8 of the
+// diagonal mass (the off-diagonal norm below 1e-4 of the diagonal's, a fifth
+// of one fp16 rounding of the stored basis): the eigenvectors then mix the
+// retained and the dropped directions by ~1e-4, which moves the
+// reconstruction error of the truncated fit by ~1e-8 relative (second
+// order), far below the fp16 and INT8 rounding of the outputs.
 // scratch: >= 2 * kThreads / 64 doubles; rot: >= kThreads / 64 * RM / 2
 // (c, s) pairs, 16-byte aligned.
 template <int RM>
@@ -1300,7 +1300,7 @@ __device__ __forceinline__ void jacobi_eig(double* Gs, double* G2, double* Ws, d
       off += part[2 * ww];
       dia += part[2 * ww + 1];
     }
-    if (off <= 1e-10 * dia || dia == 0.0) break;
+    if (off <= 1e-8 * dia || dia == 0.0) break;
     double* A = cur;
     double* B = nxt;
     int step = 0;
