@@ -231,13 +231,16 @@ def test_block_split_variants(with_logits):
         _run(states, Q, cos, sin, total - 1, "absolute", split=3, with_logits=with_logits)
 
 
-def test_records_merged_over_several_chunks():
-    """72 partial records per query head (9 cold blocks split over 8
-    workgroups each): the combine merges them 32 at a time, the last chunk
-    partly filled.  Outputs meet the oracle's bar; split 1 (10 records, one
-    chunk) agrees within a few fp16 ulps."""
-    rng = np.random.default_rng(21)
-    states = [random_state(rng, 2, 128, 9, 512, 16, 32, 100)]
+@pytest.mark.parametrize("nblk", [9, 33])
+def test_records_merged_over_several_chunks(nblk):
+    """72 or 264 partial records per query head (9 or 33 cold blocks split
+    over 8 workgroups each): the combine's waves take 64 records per round
+    (2 waves for 72 records, the second chunk partly filled; 4 waves for 264,
+    wave 0 taking two rounds) and wave 0 merges their states.  Outputs meet
+    the oracle's bar; split 1 (one record per block + tail tiles) agrees
+    within a few fp16 ulps."""
+    rng = np.random.default_rng(21 + nblk)
+    states = [random_state(rng, 2, 128, nblk, 512, 16, 32, 100)]
     total = states[0].total_tokens()
     cos, sin = rope_tables(total + 8, 128)
     Q = rng.standard_normal((1, 8, 128)).astype(np.float16)

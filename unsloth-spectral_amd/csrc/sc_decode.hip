@@ -1188,21 +1188,24 @@ __device__ __forceinline__ float chunk_reduce(float v) {
   return v;
 }
 
-template <int D, int U>
-__global__ __launch_bounds__(64) void decode_combine_kernel(DecodeParams p) {
+// NW > 1 (more than 64 records): wave w merges the chunks starting at
+// w U, w U + NW U, ..., so each wave's loads are one round; the waves' states
+// are then merged by wave 0 through LDS after one barrier.
+template <int D, int U, int NW>
+__global__ __launch_bounds__(64 * NW) void decode_combine_kernel(DecodeParams p) {
   constexpr int PREC = Geo<D>::PREC;
   constexpr int E = D / 64;  // d values per lane
   const int wq = blockIdx.x;
   const int b = wq / p.Hq, qh = wq % p.Hq;
   const int h = qh / p.nrep, hh = qh % p.nrep;
-  const int lane = threadIdx.x & 63;
+  const int lane = threadIdx.x & 63, wv = threadIdx.x >> 6;
   const int W = p.units_per_bh;
   const float* r0 = record_ptr(p, b, h, 0, hh, PREC);
   const long us = (long)p.nrep * PREC;
   float M = -INFINITY, L = 0.f, O[E];
 #pragma unroll
   for (int e = 0; e < E; ++e) O[e] = 0.f;
-  for (int u0 = 0; u0 < W; u0 += U) {
+  for (int u0 = wv * U; u0 < W; u0 += NW * U) {
     const int ku = u0 + (lane & (U - 1));
     const bool has = ku < W;
     const float* rh = r0 + (long)(has ? ku : u0) * us;
@@ -1240,6 +1243,31 @@ __global__ __launch_bounds__(64) void decode_combine_kernel(DecodeParams p) {
       for (int e = 0; e < E; ++e) O[e] = __builtin_fmaf(orr[k][e], c, O[e]);
     }
     M = mn;
+  }
+  if constexpr (NW > 1) {
+    __shared__ float st[NW][2 + E * 64];  // per wave: M, L (wave-uniform), then O[e][lane]
+    if (lane == 0) {
+      st[wv][0] = M;
+      st[wv][1] = L;
+    }
+#pragma unroll
+    for (int e = 0; e < E; ++e) st[wv][2 + e * 64 + lane] = O[e];
+    __syncthreads();
+    if (wv != 0) return;
+    float mt = -INFINITY;
+#pragma unroll
+    for (int v = 0; v < NW; ++v) mt = fmaxf(mt, st[v][0]);
+    L = 0.f;
+#pragma unroll
+    for (int e = 0; e < E; ++e) O[e] = 0.f;
+#pragma unroll
+    for (int v = 0; v < NW; ++v) {
+      const float mv = st[v][0];
+      const float a = mv == -INFINITY ? 0.f : fast_exp2(mv - mt);  // a wave that saw no token adds nothing
+      L = __builtin_fmaf(st[v][1], a, L);
+#pragma unroll
+      for (int e = 0; e < E; ++e) O[e] = __builtin_fmaf(st[v][2 + e * 64 + lane], a, O[e]);
+    }
   }
   h16* o = p.out + b * p.out_sb + (long)qh * p.out_sh + E * lane;
 #pragma unroll
@@ -1400,10 +1428,17 @@ int launch(DecodeParams& p, hipStream_t s) {
     int rc = sc_launch_status("decode_partial_kernel");
     if (rc) return rc;
   }
-  if (p.units_per_bh > 32)
-    hipLaunchKernelGGL((decode_combine_kernel<D, 64>), dim3(p.B * p.Hq), dim3(64), 0, s, p);
+  const int W = p.units_per_bh, nw = (W + 63) / 64;
+  if (nw >= 4)
+    hipLaunchKernelGGL((decode_combine_kernel<D, 64, 4>), dim3(p.B * p.Hq), dim3(256), 0, s, p);
+  else if (nw == 3)
+    hipLaunchKernelGGL((decode_combine_kernel<D, 64, 3>), dim3(p.B * p.Hq), dim3(192), 0, s, p);
+  else if (nw == 2)
+    hipLaunchKernelGGL((decode_combine_kernel<D, 64, 2>), dim3(p.B * p.Hq), dim3(128), 0, s, p);
+  else if (W > 32)
+    hipLaunchKernelGGL((decode_combine_kernel<D, 64, 1>), dim3(p.B * p.Hq), dim3(64), 0, s, p);
   else
-    hipLaunchKernelGGL((decode_combine_kernel<D, 32>), dim3(p.B * p.Hq), dim3(64), 0, s, p);
+    hipLaunchKernelGGL((decode_combine_kernel<D, 32, 1>), dim3(p.B * p.Hq), dim3(64), 0, s, p);
   return sc_launch_status("decode_combine_kernel");
 }
 
