@@ -48,7 +48,7 @@ constexpr int kWaves = 4;
 constexpr int kThreads = 64 * kWaves;
 constexpr int kTile = 16;
 constexpr int kMaxRep = 16;
-constexpr long kFillUnits = 512;  // two resident workgroups per CU on 256 CUs
+constexpr long kFillUnits = 256;  // a split grid stops at one workgroup per CU (256 CUs)
 // A CU's wave arbiter favours its oldest waves: of two resident workgroups,
 // the one dispatched second runs at about half the speed of the first and
 // finishes ~8 us after it (batch 8, 16K context).  It raises its priority
@@ -1347,9 +1347,12 @@ int fill_params(const ScDecodeArgs* a, DecodeParams* p) {
   const int tail_tiles_grid = (a->grid_tail + kTile - 1) / kTile;
   p->fold_tail = a->grid_tail > 0;
   // A cold block is split over `split` workgroups (consecutive 64-token
-  // ranges each) while the grid holds fewer than kFillUnits workgroups:
-  // small batches would otherwise leave most CUs idle while a few
-  // workgroups walk whole blocks.
+  // ranges each) while the doubled grid still holds at most kFillUnits
+  // workgroups: small batches would otherwise leave most CUs idle while a
+  // few workgroups walk whole blocks, and beyond one workgroup per CU the
+  // extra workgroups' fixed cost (bases, tail tile, record, a longer merge)
+  // outweighs the shorter walk (same-process sweeps over batch 1-4 and 4K-33K
+  // contexts: this bound picked the fastest split in every case).
   const int ranges = t->block_size / (kTile * tpw);
   const long base_units = (long)a->grid_blocks * t->batch * ((t->kv_heads + kWaves - 1) / kWaves);
   if (a->split < 0 || ranges % (a->split > 0 ? a->split : 1) || (a->split & (a->split - 1)))
