@@ -317,7 +317,8 @@ class SpectralCache:
             if not isinstance(position_ids, torch.Tensor):
                 position_ids = torch.as_tensor(position_ids)
             pos = position_ids.reshape(-1, T)
-            if pos.dtype == torch.int64 and pos.device == self.device and pos.shape[0] == B and \
+            # (the counters' device carries the index that self.device may lack)
+            if pos.dtype == torch.int64 and pos.device == self.counters.device and pos.shape[0] == B and \
                     pos.is_contiguous():
                 flags |= _lib.SC_APPEND_POS_I64     # a model's position ids as they are (no conversion launch)
             else:
