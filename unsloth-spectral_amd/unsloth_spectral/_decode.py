@@ -39,7 +39,8 @@ def _halves_equal(cos, sin):
 
 
 def _as_table(t, D):
-    t = t.to(torch.float16)
+    if t.dtype != torch.float16:
+        t = t.to(torch.float16)
     if t.dim() != 2 or t.shape[-1] != D:
         raise ValueError(f"RoPE table must be [max_len, {D}], got {tuple(t.shape)}")
     if t.stride(-1) != 1 or t.stride(0) % 8 or t.data_ptr() % 16:
@@ -89,7 +90,7 @@ def run_decode(Q, cache, cos, sin, query_position, attention_mask=None, scale=No
 
     a = _lib.ScDecodeArgs()
     tier = cache._tier()
-    a.tier = ctypes.pointer(tier)
+    a.tier = cache._tier_ptr()
     a.q_heads = Hq
     a.rope_mode = rope_mode
     a.grid_blocks = cache._n_cold

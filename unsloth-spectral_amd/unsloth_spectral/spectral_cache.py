@@ -202,7 +202,13 @@ class SpectralCache:
                          "basis_k", "basis_v", "block_start", "tail_k", "tail_v", "tail_pos", "counters"):
                 setattr(d, name, getattr(self, name).data_ptr())
             self._desc = d
+            self._desc_ptr = ctypes.pointer(d)
         return self._desc
+
+    def _tier_ptr(self):
+        """ctypes pointer to the current descriptor (kept with it)."""
+        self._tier()
+        return self._desc_ptr
 
     def _grow_cold(self, need):
         if need <= self._max_blocks:
@@ -304,8 +310,8 @@ class SpectralCache:
             if flags:
                 self.counters.zero_()
             return
-        K16 = K_new.to(torch.float16)
-        V16 = V_new.to(torch.float16)
+        K16 = K_new if K_new.dtype == torch.float16 else K_new.to(torch.float16)
+        V16 = V_new if V_new.dtype == torch.float16 else V_new.to(torch.float16)
         if K16.stride(-1) != 1 or K16.stride(2) % 8 or K16.stride(1) % 8 or K16.stride(0) % 8 or \
                 K16.data_ptr() % 16:
             K16 = K16.contiguous()
@@ -317,8 +323,7 @@ class SpectralCache:
             if not isinstance(position_ids, torch.Tensor):
                 position_ids = torch.as_tensor(position_ids)
             pos = position_ids.reshape(-1, T)
-            # (the counters' device carries the index that self.device may lack)
-            if pos.dtype == torch.int64 and pos.device == self.counters.device and pos.shape[0] == B and \
+            if pos.dtype == torch.int64 and pos.device == self.device and pos.shape[0] == B and \
                     pos.is_contiguous():
                 flags |= _lib.SC_APPEND_POS_I64     # a model's position ids as they are (no conversion launch)
             else:
@@ -326,7 +331,7 @@ class SpectralCache:
                 pos = pos.expand(B, T).contiguous() if pos.shape[0] != B else pos.contiguous()
         self._grow_tail(self._tail_len + T)
         st = _lib.stream_of(K16)
-        check(_lib.load().sc_tier_append(ctypes.byref(self._tier()), ptr(K16), ptr(V16), K16.stride(0),
+        check(_lib.load().sc_tier_append(self._tier_ptr(), ptr(K16), ptr(V16), K16.stride(0),
                                          K16.stride(1), K16.stride(2), ptr(pos), T, flags, st))
         self.total_tokens += T
         self.current_position += T
