@@ -1,7 +1,8 @@
 """Graph-replayed decode steps (CapturedDecode) against eager steps.
 
 A patched transformers MistralForCausalLM (random fp16 weights; 2 layers,
-8 query / 2 KV heads of dim 128) runs a 600-token prompt (one cold block
+8 query / 2 KV heads of dim 128, or 32 / 8 for the branch-free decode
+kernel) runs a 600-token prompt (one cold block
 plus an 88-token tail per layer) for one or two sequences, then 12
 teacher-forced one-token steps three ways from the same cache state:
   * CapturedDecode: one eager warm-up step, one capture, ten replays, with
@@ -20,10 +21,10 @@ pytestmark = pytest.mark.gpu
 VOCAB = 512
 
 
-def _model(seed=5):
+def _model(seed=5, heads=(8, 2)):
     from transformers import MistralConfig, MistralForCausalLM
     cfg = MistralConfig(vocab_size=VOCAB, hidden_size=256, intermediate_size=512, num_hidden_layers=2,
-                        num_attention_heads=8, num_key_value_heads=2, head_dim=128,
+                        num_attention_heads=heads[0], num_key_value_heads=heads[1], head_dim=128,
                         max_position_embeddings=4096, rope_theta=1e6, sliding_window=None)
     cfg._attn_implementation = "eager"
     torch.manual_seed(seed)
@@ -39,11 +40,11 @@ def _restore(model, caches):
         layer.self_attn._spectral_cache = c.clone()
 
 
-@pytest.mark.parametrize("batch", [1, 2])
+@pytest.mark.parametrize("batch,heads", [(1, (8, 2)), (2, (8, 2)), (2, (32, 8))])
 @torch.no_grad()
-def test_captured_decode_replays_match_eager_steps(batch):
+def test_captured_decode_replays_match_eager_steps(batch, heads):
     from unsloth_spectral import CapturedDecode, _lib, patch_unsloth_attention
-    model = _model()
+    model = _model(heads=heads)   # 32/8 heads: the branch-free decode kernel of the model loop
     n_prompt, steps = 600, 12
     g = torch.Generator().manual_seed(6)
     ids = torch.randint(0, VOCAB, (batch, n_prompt + steps), generator=g).cuda()
