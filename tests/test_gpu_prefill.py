@@ -94,6 +94,33 @@ def test_prefill_shuffled_query_positions():
     _check(out[0].float().cpu().numpy(), _closed_form(Q[0], states[0], cos, sin, qpos[0]))
 
 
+@pytest.mark.parametrize("ranks", [(16, 16), (32, 32)])
+def test_prefill_rows_do_not_depend_on_the_other_queries(ranks):
+    """A query's output is bit-identical whether it is prefilled with the
+    whole prompt or in a chunk of its own: the kernel groups consecutive
+    queries into workgroups and scans key tiles up to the last query of the
+    group, so a query also passes key tiles that are entirely after its own
+    position; those must leave its softmax state exactly unchanged.  Queries
+    are scaled so that the running maxima reach |m log2(e)| >= 2, where a
+    rescale factor computed as exp2 of the rounding error of m log2(e) would
+    round to 1 +- 2^-23 instead of 1."""
+    from unsloth_spectral._prefill import run_prefill
+    rng = np.random.default_rng(41)
+    states = [random_state(rng, 8, 128, 2, 512, ranks[0], ranks[1], 200, per_row=True)]
+    total = states[0].total_tokens()
+    cos, sin = rope_tables(total + 16, 128)
+    ct, sn = tables(cos, sin)
+    cache = cache_from_states(states, block_size=512)
+    Q = torch.from_numpy((4.0 * rng.standard_normal((1, 32, total, 128))).astype(np.float16)).cuda()
+    pos = torch.arange(total, device="cuda")[None]
+    full = run_prefill(Q, cache, ct, sn, pos)
+    for a, b in ((0, 37), (5, 42), (300, 301), (700, 813), (total - 53, total)):
+        part = run_prefill(Q[:, :, a:b].contiguous(), cache, ct, sn, pos[:, a:b].contiguous())
+        torch.cuda.synchronize()
+        diff = int((part != full[:, :, a:b]).sum())
+        assert diff == 0, f"queries {a}:{b}: {diff} outputs differ from the whole-prompt prefill"
+
+
 def test_prefill_matches_dense_reference_path():
     """Against integration._dense_prefill (dense fp16 attention over get_kv,
     the reference's own prefill arithmetic) on the GPU."""

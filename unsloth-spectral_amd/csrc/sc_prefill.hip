@@ -6,10 +6,11 @@
 // their absolute positions with apply_rope, spectral_attention.py:80-114,
 // which uses the first half of the cos/sin rows for both halves).
 //
-// Workgroup = (sequence b, KV head h, 32 query tokens); its four waves are
-// the four query heads of h (GQA group of 4), each over two 16-query
-// sub-tiles, so every reconstructed key tile serves 128 (query, head)
-// pairs.  Per 16-token key tile:
+// Workgroup = (sequence b, KV head h, 48 or 32 query tokens); its four waves
+// are the four query heads of h (GQA group of 4), each over three 16-query
+// sub-tiles at padded ranks 16/16 and two at larger ranks, so every
+// reconstructed key tile serves 192 or 128 (query, head) pairs.  Per
+// 16-token key tile:
 //   * cold block: the waves reconstruct K^T = B_K . C^T on MFMA from the
 //     INT8 codes (coefficients fp16(code * scale), as the reference stores
 //     them), two 16-row d tiles each (d and d + 64, so every RoPE pair is
@@ -30,9 +31,11 @@
 namespace {
 
 constexpr int kThreads = 256;
-constexpr int kQS = 2;             // 16-query sub-tiles per wave
 constexpr float kLog2e = 1.4426950408889634f;
-constexpr int kQT = 16 * kQS;      // query tokens per workgroup
+// 16-query sub-tiles per wave: three at padded ranks 16/16 (8192-token
+// prompt, 16 cold blocks: 1.231 -> 1.113 ms, in spite of 14 spilled VGPRs),
+// two at larger ranks (three spill 38 VGPRs or more); four spill 116.
+constexpr int qs_for(int kk, int kv) { return kk + kv <= 32 ? 3 : 2; }
 constexpr int kKT = 16;            // key tokens per tile
 constexpr int kPitch = 128 + 8;    // LDS row pitch (halves) of a K or V tile
 constexpr int kTile = kKT * kPitch;  // halves per LDS tile
@@ -98,6 +101,8 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(2))) v
   // Causal work grows with the query tile: workgroups are dispatched
   // heaviest first (last query tile of every (sequence, head) first), so
   // the light ones fill in at the end instead of a heavy one trailing.
+  constexpr int kQS = qs_for(KK, KV);
+  constexpr int kQT = 16 * kQS;
   const int nbh = p.t.batch * p.t.kv_heads;
   const int qt = p.nqt - 1 - (int)(blockIdx.x / nbh);
   const int bh = blockIdx.x % nbh;
@@ -183,9 +188,14 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(2))) v
       pp[u] = (half4_t)(h16)0;
       if (mn != -INFINITY) {
         // base 2: exp(x - mn) = exp2(x log2e - mn log2e); masked scores (-inf)
-        // and the first tile's m = -inf give exp2(-inf) = 0
+        // and the first tile's m = -inf give exp2(-inf) = 0.  Where the maximum
+        // did not grow the factor is set to 1: the fused form would be
+        // exp2 of the rounding error of m log2e (1 +- 2^-23 for |m log2e| >= 2),
+        // which rescaled l on every tile, fully masked ones included, and not
+        // the accumulators, so results drifted with the number of key tiles
+        // a query passed through.
         const float mnl = mn * kLog2e;
-        const float alpha = __builtin_amdgcn_exp2f(__builtin_fmaf(m[u], kLog2e, -mnl));
+        const float alpha = mn > m[u] ? __builtin_amdgcn_exp2f(__builtin_fmaf(m[u], kLog2e, -mnl)) : 1.f;
         float ls = 0.f;
 #pragma unroll
         for (int j = 0; j < 4; ++j) {
@@ -468,7 +478,8 @@ extern "C" int sc_prefill_attn(const ScPrefillArgs* a, void* stream) {
   p.t = *t;
   p.Hq = a->q_heads;
   p.Tq = a->t_q;
-  p.nqt = (a->t_q + kQT - 1) / kQT;
+  const int qt_tokens = 16 * qs_for(kk, kv);
+  p.nqt = (a->t_q + qt_tokens - 1) / qt_tokens;
   p.q = (const h16*)a->q;
   p.q_sb = a->q_stride_b;
   p.q_sh = a->q_stride_h;
