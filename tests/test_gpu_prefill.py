@@ -94,7 +94,7 @@ def test_prefill_shuffled_query_positions():
     _check(out[0].float().cpu().numpy(), _closed_form(Q[0], states[0], cos, sin, qpos[0]))
 
 
-@pytest.mark.parametrize("ranks", [(16, 16), (32, 32)])
+@pytest.mark.parametrize("ranks", [(16, 16), (32, 16), (16, 32), (32, 32)])
 def test_prefill_rows_do_not_depend_on_the_other_queries(ranks):
     """A query's output is bit-identical whether it is prefilled with the
     whole prompt or in a chunk of its own: the kernel groups consecutive

@@ -8,7 +8,7 @@
 //
 // Workgroup = (sequence b, KV head h, 48 or 32 query tokens); its four waves
 // are the four query heads of h (GQA group of 4), each over three 16-query
-// sub-tiles at padded ranks 16/16 and two at larger ranks, so every
+// sub-tiles at padded value rank 16 (key rank 16 or 32) and two otherwise, so every
 // reconstructed key tile serves 192 or 128 (query, head) pairs.  Per
 // 16-token key tile:
 //   * cold block: the waves reconstruct K^T = B_K . C^T on MFMA from the
@@ -32,10 +32,12 @@ namespace {
 
 constexpr int kThreads = 256;
 constexpr float kLog2e = 1.4426950408889634f;
-// 16-query sub-tiles per wave: three at padded ranks 16/16 (8192-token
-// prompt, 16 cold blocks: 1.231 -> 1.113 ms, in spite of 14 spilled VGPRs),
-// two at larger ranks (three spill 38 VGPRs or more); four spill 116.
-constexpr int qs_for(int kk, int kv) { return kk + kv <= 32 ? 3 : 2; }
+// 16-query sub-tiles per wave, by padded key / value rank (8192-token
+// prompt, 16 cold blocks, same-process timings): three at 16/16
+// (1.231 -> 1.113 ms, in spite of 14 spilled VGPRs) and 32/16
+// (1.231 -> 1.132 ms, 20 spilled); two at 16/32, where three spill 31 and
+// run slower (1.363 -> 1.558 ms), and at the larger ranks; four spill 116.
+constexpr int qs_for(int kk, int kv) { return kv == 16 && kk <= 32 ? 3 : 2; }
 constexpr int kKT = 16;            // key tokens per tile
 constexpr int kPitch = 128 + 8;    // LDS row pitch (halves) of a K or V tile
 constexpr int kTile = kKT * kPitch;  // halves per LDS tile
