@@ -8,7 +8,7 @@
 //
 // Workgroup = (sequence b, KV head h, 48 or 32 query tokens); its four waves
 // are the four query heads of h (GQA group of 4), each over three 16-query
-// sub-tiles at padded value rank 16 (key rank 16 or 32) and two otherwise, so every
+// sub-tiles at padded ranks 16/16, 32/16 and 16/32 and two otherwise, so every
 // reconstructed key tile serves 192 or 128 (query, head) pairs.  Per
 // 16-token key tile:
 //   * cold block: the waves reconstruct K^T = B_K . C^T on MFMA from the
@@ -33,11 +33,13 @@ namespace {
 constexpr int kThreads = 256;
 constexpr float kLog2e = 1.4426950408889634f;
 // 16-query sub-tiles per wave, by padded key / value rank (8192-token
-// prompt, 16 cold blocks, same-process timings): three at 16/16
-// (1.231 -> 1.113 ms, in spite of 14 spilled VGPRs) and 32/16
-// (1.231 -> 1.132 ms, 20 spilled); two at 16/32, where three spill 31 and
-// run slower (1.363 -> 1.558 ms), and at the larger ranks; four spill 116.
-constexpr int qs_for(int kk, int kv) { return kv == 16 && kk <= 32 ? 3 : 2; }
+// prompt, 16 cold blocks, same-process timings against two sub-tiles):
+// three at 16/16, 32/16 and 16/32, with the cold-tile inputs fetched one
+// tile ahead instead of two (6, 12 and 22 spilled VGPRs): 1.231 -> 1.045,
+// 1.231 -> 1.080 and 1.356 -> 1.168 ms.  With inputs two tiles ahead three
+// sub-tiles spill 14, 20 and 31 (1.113, 1.132 and 1.558 ms).  Two at the
+// larger ranks (no spills); four spill 116.
+constexpr int qs_for(int kk, int kv) { return (kv == 16 && kk <= 32) || (kk == 16 && kv == 32) ? 3 : 2; }
 constexpr int kKT = 16;            // key tokens per tile
 constexpr int kPitch = 128 + 8;    // LDS row pitch (halves) of a K or V tile
 constexpr int kTile = kKT * kPitch;  // halves per LDS tile
@@ -105,6 +107,7 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(2))) v
   // the light ones fill in at the end instead of a heavy one trailing.
   constexpr int kQS = qs_for(KK, KV);
   constexpr int kQT = 16 * kQS;
+  constexpr bool kShallow = kQS == 3;  // cold-tile inputs one tile ahead (fewer live registers)
   const int nbh = p.t.batch * p.t.kv_heads;
   const int qt = p.nqt - 1 - (int)(blockIdx.x / nbh);
   const int bh = blockIdx.x % nbh;
@@ -306,21 +309,31 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(2))) v
     // Software pipeline over the tiles: tile tt + 1 is reconstructed into
     // the other LDS buffer before tile tt's scores and values (independent
     // work the scheduler can interleave), with one barrier per tile; the
-    // global inputs run two tiles ahead of their reconstruction.
+    // global inputs run two tiles ahead of their reconstruction.  With
+    // kShallow they run one tile ahead: tile tt + 1's loads are issued
+    // before tile tt's scores, which cover their latency, and the tile is
+    // reconstructed after them (one set of inputs fewer in registers).
     TileIn cur, nxt, nx2;
     load_in(0, cur);
-    if (ntl > 1) load_in(kKT, nxt);
+    if (!kShallow && ntl > 1) load_in(kKT, nxt);
     recon(cur, buf);
     __syncthreads();
     for (int tt = 0; tt < ntl; ++tt) {
       const int tok0 = tt * kKT;
-      if (tt + 2 < ntl) load_in(tok0 + 2 * kKT, nx2);
-      if (tt + 1 < ntl) recon(nxt, buf ^ 1);
+      if constexpr (kShallow) {
+        if (tt + 1 < ntl) load_in(tok0 + kKT, nxt);
+      } else {
+        if (tt + 2 < ntl) load_in(tok0 + 2 * kKT, nx2);
+        if (tt + 1 < ntl) recon(nxt, buf ^ 1);
+      }
       int kpos[4];
 #pragma unroll
       for (int e = 0; e < 4; ++e) kpos[e] = start + tok0 + 4 * g + e;
       half4_t pp[kQS];
       scores(kpos, start + tok0 + kKT - 1, pp);
+      if constexpr (kShallow) {
+        if (tt + 1 < ntl) recon(nxt, buf ^ 1);
+      }
       // ---- values in rank space: O_k^T[16 nt + n][q] += C_V[tok 4g + e][16 nt + n] * P[tok][q]
 #pragma unroll
       for (int nt = 0; nt < NTV; ++nt) {
@@ -333,7 +346,7 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(2))) v
       __syncthreads();  // tile tt read by every wave; tile tt + 1 written
       buf ^= 1;
       cur = nxt;
-      nxt = nx2;
+      if constexpr (!kShallow) nxt = nx2;
     }
     // ---- projection of the block: O_d^T[d][q] += B_V[d][k] O_k^T[k][q] (hi + lo fp16 parts)
     half4_t ph[kQS][NTV], pl[kQS][NTV];
